@@ -1,0 +1,339 @@
+"""ctypes wrapper around liboracle.so, the CPU restatement of the reference's
+Ligero commit arithmetic.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker.  The product path
+(volta-zk_amd/volta_mi355x) never imports this module.
+
+Function-level citations of the reference live in volta_oracle.h/.c.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import subprocess
+
+import numpy as np
+
+P = 0xFFFF_FFFF_0000_0001
+EPS = 0xFFFF_FFFF
+FNV_OFFSET = 0xCBF2_9CE4_8422_2325
+
+_HERE = pathlib.Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+
+FP2_DTYPE = np.dtype([("c0", "<u8"), ("c1", "<u8")])
+
+
+class Fp2C(ctypes.Structure):
+    _fields_ = [("c0", ctypes.c_uint64), ("c1", ctypes.c_uint64)]
+
+
+def build(force: bool = False) -> None:
+    """Compile liboracle.so with the committed Makefile."""
+    if force or not _LIB_PATH.exists():
+        subprocess.run(["make", "-B" if force else "-s", "-C", str(_HERE)], check=True,
+                       stdout=subprocess.DEVNULL)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not _LIB_PATH.exists():
+            build()
+        _lib = ctypes.CDLL(str(_LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    u64, sz, i32 = ctypes.c_uint64, ctypes.c_size_t, ctypes.c_int
+    vp = ctypes.c_void_p
+    sig = {
+        "vo_fp_new": (u64, [u64]),
+        "vo_fp_from_i64": (u64, [ctypes.c_int64]),
+        "vo_fp_add": (u64, [u64, u64]),
+        "vo_fp_sub": (u64, [u64, u64]),
+        "vo_fp_neg": (u64, [u64]),
+        "vo_fp_mul": (u64, [u64, u64]),
+        "vo_fp_pow": (u64, [u64, u64]),
+        "vo_fp_inv": (u64, [u64]),
+        "vo_fp2_mul": (Fp2C, [Fp2C, Fp2C]),
+        "vo_fp2_add": (Fp2C, [Fp2C, Fp2C]),
+        "vo_fp2_mul_base": (Fp2C, [Fp2C, u64]),
+        "vo_fp_mul_vec": (None, [vp, vp, vp, sz]),
+        "vo_fp_add_vec": (None, [vp, vp, vp, sz]),
+        "vo_fp_sub_vec": (None, [vp, vp, vp, sz]),
+        "vo_root_of_unity": (u64, [ctypes.c_uint32]),
+        "vo_ntt_twiddles": (None, [sz, vp]),
+        "vo_ntt_forward": (None, [vp, sz, vp]),
+        "vo_ntt_encode_batch": (None, [vp, sz, sz, sz, vp, i32]),
+        "vo_ntt_forward_batch": (None, [vp, sz, sz, i32]),
+        "vo_ntt_inverse_batch": (None, [vp, sz, sz, i32]),
+        "vo_pcs_messages": (None, [vp, vp, sz, sz, sz, sz, vp, i32]),
+        "vo_pcs_encode_i16": (None, [vp, vp, sz, sz, sz, sz, vp, i32]),
+        "vo_pcs_combine_rows": (None, [vp, vp, vp, sz, sz, sz, sz, vp, i32]),
+        "vo_combine_rows_fp": (None, [vp, vp, sz, sz, sz, vp, i32]),
+        "vo_fp2_powers": (None, [Fp2C, sz, vp]),
+        "vo_fp2_add_inplace": (None, [vp, vp, sz]),
+        "vo_gather_columns": (None, [vp, sz, sz, vp, sz, vp]),
+        "vo_gather_fp2_columns": (None, [vp, sz, sz, vp, sz, vp]),
+        "vo_fp_rows": (None, [vp, u64, sz, sz, vp, i32]),
+        "vo_fp2_rows_padded": (None, [vp, u64, sz, sz, sz, vp, i32]),
+        "vo_raw_u64": (None, [vp, u64, sz, vp]),
+        "vo_fnv_u64": (u64, [vp, sz, u64]),
+        "vo_fp2_mul_stream": (None, [vp, vp, vp, sz, i32]),
+        "vo_fp2_chain": (None, [vp, vp, vp, sz, i32, i32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def default_threads() -> int:
+    """Cores available to this process (cgroup/affinity aware)."""
+    try:
+        return max(1, len(os.sched_getaffinity(0)))
+    except AttributeError:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _fp2_array(a) -> np.ndarray:
+    a = np.ascontiguousarray(a)
+    if a.dtype == FP2_DTYPE:
+        return a
+    a = np.ascontiguousarray(a, dtype=np.uint64)
+    assert a.shape[-1] == 2
+    return a.view(FP2_DTYPE).reshape(a.shape[:-1])
+
+
+def fp2_to_u64(a: np.ndarray) -> np.ndarray:
+    """View an Fp2 array as (..., 2) uint64."""
+    return np.ascontiguousarray(a).view(np.uint64).reshape(a.shape + (2,))
+
+
+# ---- scalar field -----------------------------------------------------------
+
+def fp_new(x: int) -> int: return lib().vo_fp_new(x)
+def fp_from_i64(x: int) -> int: return lib().vo_fp_from_i64(x)
+def fp_add(a: int, b: int) -> int: return lib().vo_fp_add(a, b)
+def fp_sub(a: int, b: int) -> int: return lib().vo_fp_sub(a, b)
+def fp_neg(a: int) -> int: return lib().vo_fp_neg(a)
+def fp_mul(a: int, b: int) -> int: return lib().vo_fp_mul(a, b)
+def fp_pow(a: int, e: int) -> int: return lib().vo_fp_pow(a, e)
+def fp_inv(a: int) -> int: return lib().vo_fp_inv(a)
+
+
+def fp2_mul(a, b):
+    r = lib().vo_fp2_mul(Fp2C(*a), Fp2C(*b))
+    return (r.c0, r.c1)
+
+
+def fp2_add(a, b):
+    r = lib().vo_fp2_add(Fp2C(*a), Fp2C(*b))
+    return (r.c0, r.c1)
+
+
+def fp2_mul_base(a, x: int):
+    r = lib().vo_fp2_mul_base(Fp2C(*a), x)
+    return (r.c0, r.c1)
+
+
+def _vec_op(name: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint64)
+    b = np.ascontiguousarray(b, dtype=np.uint64)
+    out = np.empty_like(a)
+    getattr(lib(), name)(_ptr(a), _ptr(b), _ptr(out), a.size)
+    return out
+
+
+def fp_mul_vec(a, b): return _vec_op("vo_fp_mul_vec", a, b)
+def fp_add_vec(a, b): return _vec_op("vo_fp_add_vec", a, b)
+def fp_sub_vec(a, b): return _vec_op("vo_fp_sub_vec", a, b)
+
+
+# ---- NTT ----------------------------------------------------------------------
+
+def root_of_unity(bits: int) -> int:
+    return lib().vo_root_of_unity(bits)
+
+
+def ntt_twiddles(n: int) -> np.ndarray:
+    tw = np.empty(max(1, n // 2), dtype=np.uint64)
+    lib().vo_ntt_twiddles(n, _ptr(tw))
+    return tw[: n // 2]
+
+
+def ntt_encode_batch(msgs: np.ndarray, n: int, threads: int | None = None) -> np.ndarray:
+    msgs = np.ascontiguousarray(msgs, dtype=np.uint64)
+    rows, msg_len = msgs.shape
+    out = np.empty((rows, n), dtype=np.uint64)
+    lib().vo_ntt_encode_batch(_ptr(msgs), rows, msg_len, n, _ptr(out),
+                              threads or default_threads())
+    return out
+
+
+def ntt_forward_batch(data: np.ndarray, threads: int | None = None) -> np.ndarray:
+    out = np.array(data, dtype=np.uint64, order="C", copy=True)
+    rows, n = out.shape
+    lib().vo_ntt_forward_batch(_ptr(out), rows, n, threads or default_threads())
+    return out
+
+
+def ntt_inverse_batch(data: np.ndarray, threads: int | None = None) -> np.ndarray:
+    out = np.array(data, dtype=np.uint64, order="C", copy=True)
+    rows, n = out.shape
+    lib().vo_ntt_inverse_batch(_ptr(out), rows, n, threads or default_threads())
+    return out
+
+
+# ---- PCS rows ----------------------------------------------------------------
+
+def _pads_or_dummy(pads, rows, pad):
+    if pad == 0:
+        return np.zeros(1, dtype=np.uint64)
+    pads = np.ascontiguousarray(pads, dtype=np.uint64)
+    assert pads.size == rows * pad
+    return pads
+
+
+def pcs_messages(w: np.ndarray, pads, rows: int, cols: int, pad: int, code_len: int,
+                 threads: int | None = None) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.int16)
+    assert w.size == rows * cols
+    p = _pads_or_dummy(pads, rows, pad)
+    out = np.empty((rows, code_len), dtype=np.uint64)
+    lib().vo_pcs_messages(_ptr(w), _ptr(p), rows, cols, pad, code_len, _ptr(out),
+                          threads or default_threads())
+    return out
+
+
+def pcs_encode_i16(w: np.ndarray, pads, rows: int, cols: int, pad: int, code_len: int,
+                   threads: int | None = None) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.int16)
+    assert w.size == rows * cols
+    p = _pads_or_dummy(pads, rows, pad)
+    out = np.empty((rows, code_len), dtype=np.uint64)
+    lib().vo_pcs_encode_i16(_ptr(w), _ptr(p), rows, cols, pad, code_len, _ptr(out),
+                            threads or default_threads())
+    return out
+
+
+def pcs_combine_rows(w: np.ndarray, pads, coeffs, rows: int, cols: int, pad: int,
+                     combinations: int, threads: int | None = None) -> np.ndarray:
+    """Returns (combinations, cols+pad) Fp2 as a (..., 2) uint64 array."""
+    w = np.ascontiguousarray(w, dtype=np.int16)
+    p = _pads_or_dummy(pads, rows, pad)
+    c = _fp2_array(coeffs).reshape(-1)
+    assert c.size == combinations * rows
+    out = np.empty((combinations, cols + pad), dtype=FP2_DTYPE)
+    lib().vo_pcs_combine_rows(_ptr(w), _ptr(p), _ptr(c), rows, cols, pad, combinations,
+                              _ptr(out), threads or default_threads())
+    return fp2_to_u64(out)
+
+
+def combine_rows_fp(msgs: np.ndarray, coeffs, combinations: int,
+                    threads: int | None = None) -> np.ndarray:
+    msgs = np.ascontiguousarray(msgs, dtype=np.uint64)
+    rows, cols = msgs.shape
+    c = _fp2_array(coeffs).reshape(-1)
+    assert c.size == combinations * rows
+    out = np.empty((combinations, cols), dtype=FP2_DTYPE)
+    lib().vo_combine_rows_fp(_ptr(msgs), _ptr(c), rows, cols, combinations, _ptr(out),
+                             threads or default_threads())
+    return fp2_to_u64(out)
+
+
+def fp2_powers(base, count: int) -> np.ndarray:
+    out = np.empty(count, dtype=FP2_DTYPE)
+    lib().vo_fp2_powers(Fp2C(*base), count, _ptr(out))
+    return fp2_to_u64(out)
+
+
+def fp2_add_inplace(target: np.ndarray, add: np.ndarray) -> np.ndarray:
+    t = _fp2_array(np.array(target, dtype=np.uint64, copy=True)).reshape(-1).copy()
+    a = _fp2_array(add).reshape(-1)
+    lib().vo_fp2_add_inplace(_ptr(t), _ptr(a), t.size)
+    return fp2_to_u64(t)
+
+
+def gather_columns(m: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    m = np.ascontiguousarray(m, dtype=np.uint64)
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    rows, cols = m.shape
+    out = np.empty((idx.size, rows), dtype=np.uint64)
+    lib().vo_gather_columns(_ptr(m), rows, cols, _ptr(idx), idx.size, _ptr(out))
+    return out
+
+
+def gather_fp2_columns(m: np.ndarray, idx: np.ndarray) -> np.ndarray:
+    mm = _fp2_array(m)
+    rows, cols = mm.shape
+    idx = np.ascontiguousarray(idx, dtype=np.uint32)
+    out = np.empty((idx.size, rows), dtype=FP2_DTYPE)
+    lib().vo_gather_fp2_columns(_ptr(mm), rows, cols, _ptr(idx), idx.size, _ptr(out))
+    return fp2_to_u64(out)
+
+
+# ---- FpStream -----------------------------------------------------------------
+
+def _seed(seed) -> np.ndarray:
+    s = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+    assert s.size == 32
+    return s
+
+
+def fp_rows(seed, base_domain: int, rows: int, count: int,
+            threads: int | None = None) -> np.ndarray:
+    s = _seed(seed)
+    out = np.empty((rows, count), dtype=np.uint64)
+    lib().vo_fp_rows(_ptr(s), base_domain, rows, count, _ptr(out), threads or default_threads())
+    return out
+
+
+def fp2_rows_padded(seed, base_domain: int, rows: int, count: int, padded: int,
+                    threads: int | None = None) -> np.ndarray:
+    s = _seed(seed)
+    out = np.empty((rows, padded), dtype=FP2_DTYPE)
+    lib().vo_fp2_rows_padded(_ptr(s), base_domain, rows, count, padded, _ptr(out),
+                             threads or default_threads())
+    return fp2_to_u64(out)
+
+
+def raw_u64(seed, domain: int, count: int) -> np.ndarray:
+    s = _seed(seed)
+    out = np.empty(count, dtype=np.uint64)
+    lib().vo_raw_u64(_ptr(s), domain, count, _ptr(out))
+    return out
+
+
+# ---- checksums / spike kernels ---------------------------------------------------
+
+def fnv(values: np.ndarray, h: int = FNV_OFFSET) -> int:
+    v = np.ascontiguousarray(values).view(np.uint64).reshape(-1)
+    return lib().vo_fnv_u64(_ptr(v), v.size, h)
+
+
+def fp2_mul_stream(a, b, threads: int | None = None) -> np.ndarray:
+    a, b = _fp2_array(a).reshape(-1), _fp2_array(b).reshape(-1)
+    out = np.empty_like(a)
+    lib().vo_fp2_mul_stream(_ptr(a), _ptr(b), _ptr(out), a.size, threads or default_threads())
+    return fp2_to_u64(out)
+
+
+def fp2_chain(a, b, rounds: int, threads: int | None = None) -> np.ndarray:
+    a, b = _fp2_array(a).reshape(-1), _fp2_array(b).reshape(-1)
+    out = np.empty_like(a)
+    lib().vo_fp2_chain(_ptr(a), _ptr(b), _ptr(out), a.size, rounds,
+                       threads or default_threads())
+    return fp2_to_u64(out)

@@ -1,0 +1,279 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each check is chosen so a plausible restatement mistake (dropped carry term,
+wrong twiddle index, transposed operand, wrong word order) fails it:
+  * reference-recorded checksums of the reference's own arithmetic runs
+    (benchmarks/results/p7-gpu-pcs-arithmetic[-quick]-2026-07-11-366ec4a.json,
+    p7-gpu-roofline[-quick]-2026-07-11-a43d105.json);
+  * the reference's unit cases (rust/volta-field/src/lib.rs:297-351,
+    rust/volta-pcs/src/ntt.rs:78-121) restated;
+  * Python big-integer arithmetic and brute-force DFTs;
+  * the ChaCha8 KAT of rust/volta-accel/src/lib.rs:7517-7528 and the
+    published all-zero-key ChaCha8 keystream.
+"""
+import random
+
+import numpy as np
+import pytest
+
+P = 0xFFFF_FFFF_0000_0001
+EPS = 0xFFFF_FFFF
+MASK64 = (1 << 64) - 1
+
+
+# ---- field ------------------------------------------------------------------
+
+def test_field_differential_against_big_ints(oracle):
+    rnd = random.Random(0xB0)
+    a = np.array([rnd.randrange(P) for _ in range(20000)], dtype=np.uint64)
+    b = np.array([rnd.randrange(P) for _ in range(20000)], dtype=np.uint64)
+    # include the boundary values
+    a[:4] = [0, 1, P - 1, P - 2]
+    b[:4] = [P - 1, P - 1, P - 1, 1]
+    mul, add, sub = oracle.fp_mul_vec(a, b), oracle.fp_add_vec(a, b), oracle.fp_sub_vec(a, b)
+    for x, y, m, s, d in zip(a.tolist(), b.tolist(), mul.tolist(), add.tolist(), sub.tolist()):
+        assert m == x * y % P
+        assert s == (x + y) % P
+        assert d == (x - y) % P
+
+
+def test_field_edge_cases(oracle):
+    # rust/volta-field/src/lib.rs:309-320
+    assert oracle.fp_mul(P - 1, P - 1) == 1
+    assert oracle.fp_add(P - 1, 1) == 0
+    assert oracle.fp_sub(0, 1) == P - 1
+    assert oracle.fp_new(MASK64) == MASK64 - P
+    assert oracle.fp_pow(2, 64) == EPS
+    assert oracle.fp_pow(2, 96) == P - 1
+    assert oracle.fp_from_i64(-5) == oracle.fp_sub(0, 5)
+    assert oracle.fp_from_i64(-32768) == P - 32768
+    assert oracle.fp_from_i64(32767) == 32767
+    assert oracle.fp_neg(0) == 0 and oracle.fp_neg(3) == P - 3
+
+
+def test_inverse_and_non_residue(oracle):
+    rnd = random.Random(1)
+    for _ in range(200):
+        a = rnd.randrange(1, P)
+        assert oracle.fp_mul(a, oracle.fp_inv(a)) == 1
+    # lib.rs:331-335: 7 is a quadratic non-residue
+    assert oracle.fp_pow(7, (P - 1) // 2) == P - 1
+
+
+def _fp2_mul_ref(a, b):
+    return ((a[0] * b[0] + 7 * a[1] * b[1]) % P, (a[0] * b[1] + a[1] * b[0]) % P)
+
+
+def test_fp2_against_big_ints(oracle):
+    rnd = random.Random(2)
+    for _ in range(500):
+        a = (rnd.randrange(P), rnd.randrange(P))
+        b = (rnd.randrange(P), rnd.randrange(P))
+        x = rnd.randrange(P)
+        assert oracle.fp2_mul(a, b) == _fp2_mul_ref(a, b)
+        assert oracle.fp2_add(a, b) == ((a[0] + b[0]) % P, (a[1] + b[1]) % P)
+        assert oracle.fp2_mul_base(a, x) == (a[0] * x % P, a[1] * x % P)
+
+
+def test_fp2_powers_start_at_c(oracle):
+    # ligero.rs:772-778: c^1 .. c^rows
+    c = (123456789, 987654321)
+    got = oracle.fp2_powers(c, 5)
+    acc = (1, 0)
+    for k in range(5):
+        acc = _fp2_mul_ref(acc, c)
+        assert tuple(int(v) for v in got[k]) == acc
+
+
+# ---- NTT ------------------------------------------------------------------------
+
+def _naive_dft(a, w):
+    n = len(a)
+    return [sum(a[i] * pow(w, i * j, P) for i in range(n)) % P for j in range(n)]
+
+
+def test_root_has_exact_order(oracle):
+    # ntt.rs:78-87
+    for bits in (1, 4, 15, 32):
+        w = oracle.root_of_unity(bits)
+        assert pow(w, 1 << (bits - 1), P) == P - 1
+        assert pow(w, 1 << bits, P) == 1
+    assert oracle.root_of_unity(5) == pow(7, (P - 1) >> 5, P)
+
+
+def test_ntt_matches_naive_dft_n16(oracle):
+    # ntt.rs:89-104: a_i = i^2 + 3
+    a = np.array([i * i + 3 for i in range(16)], dtype=np.uint64)
+    got = oracle.ntt_forward_batch(a.reshape(1, 16))[0]
+    assert got.tolist() == _naive_dft(a.tolist(), oracle.root_of_unity(4))
+
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 5, 7, 8])
+def test_ntt_matches_naive_dft_random(oracle, bits):
+    n = 1 << bits
+    rnd = random.Random(bits)
+    a = [rnd.randrange(P) for _ in range(n)]
+    got = oracle.ntt_forward_batch(np.array([a], dtype=np.uint64))[0]
+    assert got.tolist() == _naive_dft(a, pow(7, (P - 1) >> bits, P))
+
+
+def test_encode_is_polynomial_evaluation(oracle):
+    # ntt.rs:106-121: codeword[j] = poly(w^j) for a zero-padded message
+    msg = [7 * i + 1 for i in range(5)]
+    code = oracle.ntt_encode_batch(np.array([msg], dtype=np.uint64), 32)[0]
+    w = oracle.root_of_unity(5)
+    for j in (0, 1, 17, 31):
+        x = pow(w, j, P)
+        acc = 0
+        for c in reversed(msg):
+            acc = (acc * x + c) % P
+        assert int(code[j]) == acc
+
+
+def test_inverse_ntt_round_trip_and_naive(oracle):
+    rnd = random.Random(9)
+    a = np.array([[rnd.randrange(P) for _ in range(64)] for _ in range(3)], dtype=np.uint64)
+    fwd = oracle.ntt_forward_batch(a)
+    assert (oracle.ntt_inverse_batch(fwd) == a).all()
+    # a_i = n^-1 sum_j A_j w^-ij
+    n = 64
+    w_inv = pow(pow(7, (P - 1) >> 6, P), P - 2, P)
+    n_inv = pow(n, P - 2, P)
+    A = fwd[0].tolist()
+    naive = [n_inv * x % P for x in _naive_dft(A, w_inv)]
+    assert naive == a[0].tolist()
+
+
+def spike_ntt_input(rows, bits, msg_len):
+    """cuda/p7_pcs_arithmetic.cu:207-211: in[idx] = (idx*0x9E3779B9 + 17) mod p
+    for j < msg_len, idx the global row-major index."""
+    n = 1 << bits
+    idx = np.arange(rows * n, dtype=np.uint64)
+    v = (idx * np.uint64(0x9E3779B9) + np.uint64(17)) % np.uint64(P)
+    v = v.reshape(rows, n)
+    v[:, msg_len:] = 0
+    return v
+
+
+@pytest.mark.parametrize("rows,bits,msg_len,expected", [
+    (32, 12, 2304, 0xA87A560725F2D016),
+    (1024, 15, 16896, 0xBE7B90425A4C7229),
+])
+def test_ntt_reference_checksums(oracle, rows, bits, msg_len, expected):
+    out = oracle.ntt_forward_batch(spike_ntt_input(rows, bits, msg_len))
+    assert oracle.fnv(out) == expected
+
+
+def spike_combine_inputs(rows, cols):
+    """cuda/p7_pcs_arithmetic.cu:270-275."""
+    i = np.arange(rows * cols, dtype=np.uint64)
+    w = ((i * np.uint64(0x85EBCA6B) + np.uint64(29)) % np.uint64(P)).reshape(rows, cols)
+    r = np.arange(rows, dtype=np.uint64)
+    q = np.stack([(r * np.uint64(37) + np.uint64(11)) % np.uint64(P), (r * np.uint64(53) + np.uint64(5)) % np.uint64(P)], 1)
+    c = np.stack([(r * np.uint64(71) + np.uint64(7)) % np.uint64(P), (r * np.uint64(97) + np.uint64(13)) % np.uint64(P)], 1)
+    return w, q, c
+
+
+def combine_checksum(oracle, uq, uc):
+    return oracle.fnv(uq) ^ ((oracle.fnv(uc) * 0x9E3779B97F4A7C15) & MASK64)
+
+
+@pytest.mark.parametrize("rows,cols,expected", [
+    (32, 2048, 0x0852323A5805ED2C),
+    (1024, 16384, 0x856F9A96D8E01901),
+])
+def test_combination_reference_checksums(oracle, rows, cols, expected):
+    w, q, c = spike_combine_inputs(rows, cols)
+    coeffs = np.concatenate([q, c]).reshape(2 * rows, 2)
+    u = oracle.combine_rows_fp(w, coeffs, 2)
+    assert combine_checksum(oracle, u[0], u[1]) == expected
+
+
+def test_combination_brute_force_i16_with_pads(oracle):
+    rnd = random.Random(5)
+    rows, cols, pad, comb = 5, 6, 3, 2
+    w = np.array([rnd.randrange(-32768, 32768) for _ in range(rows * cols)], dtype=np.int16)
+    pads = np.array([rnd.randrange(P) for _ in range(rows * pad)], dtype=np.uint64)
+    co = np.array([[rnd.randrange(P), rnd.randrange(P)] for _ in range(comb * rows)], dtype=np.uint64)
+    got = oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)
+    for k in range(comb):
+        for j in range(cols + pad):
+            s0 = s1 = 0
+            for i in range(rows):
+                x = int(w[i * cols + j]) % P if j < cols else int(pads[i * pad + j - cols])
+                s0 += int(co[k * rows + i, 0]) * x
+                s1 += int(co[k * rows + i, 1]) * x
+            assert (int(got[k, j, 0]), int(got[k, j, 1])) == (s0 % P, s1 % P)
+
+
+def test_messages_lift_and_layout(oracle):
+    w = np.array([0, -1, 32767, -32768], dtype=np.int16)
+    pads = np.array([11, 12], dtype=np.uint64)
+    m = oracle.pcs_messages(w, pads, 2, 2, 1, 4)
+    assert m.tolist() == [[0, P - 1, 11, 0], [32767, P - 32768, 12, 0]]
+
+
+@pytest.mark.parametrize("log2,expected", [(20, 0xAB1B94B1D98FD160), (24, 0x33EB029C2CCB481F)])
+def test_fp2_stream_reference_checksums(oracle, log2, expected):
+    a, b = spike_fp2_inputs(1 << log2)
+    assert oracle.fnv(oracle.fp2_mul_stream(a, b)) == expected
+
+
+@pytest.mark.parametrize("log2,rounds,expected", [(16, 64, 0x994B7AB598EDF5D0), (20, 256, 0x2D1768754CF29569)])
+def test_fp2_chain_reference_checksums(oracle, log2, rounds, expected):
+    a, b = spike_fp2_inputs(1 << log2)
+    assert oracle.fnv(oracle.fp2_chain(a, b, rounds)) == expected
+
+
+def spike_fp2_inputs(n):
+    """cuda/p7_goldilocks_roofline.cu:112-119."""
+    x = np.arange(n, dtype=np.uint64)
+    Pu = np.uint64(P)
+    a = np.stack([(x * np.uint64(0x9E3779B9) + np.uint64(17)) % Pu, (x * np.uint64(0x85EBCA6B) + np.uint64(29)) % Pu], 1)
+    b = np.stack([(x * np.uint64(0xC2B2AE35) + np.uint64(31)) % Pu, (x * np.uint64(0x27D4EB2F) + np.uint64(43)) % Pu], 1)
+    return a, b
+
+
+# ---- FpStream / ChaCha8 ---------------------------------------------------------------
+
+KAT_SEED = bytes((17 * i + 3) % 256 for i in range(32))
+
+
+def test_chacha8_reference_kat(oracle):
+    # rust/volta-accel/src/lib.rs:7517-7528: 6th raw u64 is 0xffffffffb1461b28
+    raw = oracle.raw_u64(KAT_SEED, 0x19664BCA, 8)
+    assert int(raw[5]) == 0xFFFF_FFFF_B146_1B28
+    rows = oracle.fp_rows(KAT_SEED, 0x19664BCA, 3, 10)
+    # that draw is >= p and must be rejected, so row 0 takes raw[6] at index 5
+    assert rows[0, :5].tolist() == raw[:5].tolist()
+    assert int(rows[0, 5]) == int(raw[6])
+    assert (rows < P).all()
+
+
+def test_chacha8_published_zero_key_keystream(oracle):
+    # Bernstein ChaCha, 8 rounds, 256-bit all-zero key, zero nonce, block 0
+    raw = oracle.raw_u64(bytes(32), 0, 8)
+    assert raw.view(np.uint8).tobytes().hex() == (
+        "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+        "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+
+
+def test_stream_domain_separation_and_fp2(oracle):
+    seed = bytes([42] * 32)
+    a = oracle.fp_rows(seed, 7, 1, 32)[0]
+    b = oracle.fp_rows(seed, 7, 1, 32)[0]
+    c = oracle.fp_rows(seed, 8, 1, 32)[0]
+    assert (a == b).all() and not (a == c).all()
+    # next_fp2 = two consecutive accepted draws (c0 then c1)
+    f2 = oracle.fp2_rows_padded(seed, 7, 1, 4, 6)[0]
+    assert f2[:4].reshape(-1).tolist() == a[:8].tolist()
+    assert f2[4:].reshape(-1).tolist() == [0, 0, 0, 0]
+    # the second block continues the keystream (counter increments)
+    raw = oracle.raw_u64(seed, 7, 16)
+    assert raw[:8].tolist() != raw[8:].tolist()
+
+
+def test_gather_columns(oracle):
+    m = np.arange(24, dtype=np.uint64).reshape(4, 6)
+    idx = np.array([5, 0, 3], dtype=np.uint32)
+    assert oracle.gather_columns(m, idx).tolist() == [m[:, 5].tolist(), m[:, 0].tolist(), m[:, 3].tolist()]

@@ -1,0 +1,550 @@
+// abi_pcs.cpp -- the PCS entry points of the volta_cuda_* C ABI (ABI 37) plus
+// the MI355X extensions (volta_mi355x_*).
+//
+// Each reference entry point keeps its signature, unit conventions (element
+// offsets for compute calls, byte offsets for raw storage), geometry checks,
+// error strings and RawStats side effects; the reference implementation
+// each replaces is cited at the function.  Compute runs on the context's
+// single HIP stream; only entry points that return host data synchronise.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <vector>
+
+#include "context.hpp"
+#include "gl64.hpp"
+#include "kernels.hpp"
+
+using namespace vmx;
+using gl::Fp2;
+
+namespace {
+
+bool pow2(size_t n) { return n >= 2 && (n & (n - 1)) == 0; }
+
+template <class F>
+int guarded(Context* c, const char* what, F&& f) noexcept {
+    try {
+        return f();
+    } catch (const std::exception&) {
+        std::string m = std::string(what) + " threw a C++ exception";
+        return fail_msg(c, m.c_str());
+    } catch (...) {
+        std::string m = std::string(what) + " threw an unknown exception";
+        return fail_msg(c, m.c_str());
+    }
+}
+
+// Resident forward NTT with the per-size twiddle upload accounted as H2D.
+int resident_ntt(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
+                 uint64_t* out, bool inverse) {
+    uint64_t h2d = 0;
+    TwiddleSet* t = nullptr;
+    if (inverse ? ensure_inverse_twiddles(c, n, &h2d, &t) : ensure_twiddles(c, n, &h2d, &t)) return -1;
+    if (begin_op(c) || mark_op(c, 1)) return -1;
+    if (ntt_fp_rows(c, in, in_stride, msg_len, rows, n, out, inverse ? t->inv : t->fwd, inverse)) return -1;
+    if (mark_op(c, 2)) return -1;
+    return finish_op(c, OP_PCS_NTT, h2d, 0);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Resident NTTs
+// ---------------------------------------------------------------------------
+
+// Replaces volta_cuda_ntt_fp_batch_device (cuda/volta_cuda_backend.cu:6545-6561):
+// out-of-place batched forward NTT of pre-padded rows; input is preserved.
+VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows, size_t n,
+                                              uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident Fp NTT geometry");
+    return guarded(c, "resident Fp NTT", [&] {
+        size_t total = 0;
+        if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp NTT geometry overflows size_t");
+        void *in = nullptr, *out = nullptr;
+        if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
+            return -1;
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+            return fail_msg(c, "resident Fp NTT input and output overlap");
+        return resident_ntt(c, static_cast<const uint64_t*>(in), n, n, rows, n, static_cast<uint64_t*>(out),
+                            false);
+    });
+}
+
+// Replaces volta_cuda_ntt_fp2_batch_device (.cu:6563-6579): componentwise Fp2
+// NTT with base-field twiddles.
+VMX_API int volta_cuda_ntt_fp2_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows, size_t n,
+                                               uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident Fp2 NTT geometry");
+    return guarded(c, "resident Fp2 NTT", [&] {
+        size_t total = 0;
+        if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp2 NTT geometry overflows size_t");
+        void *in = nullptr, *out = nullptr;
+        if (region_elems(c, in_id, in_off, total, 16, &in) || region_elems(c, out_id, out_off, total, 16, &out))
+            return -1;
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+            return fail_msg(c, "resident Fp2 NTT input and output overlap");
+        uint64_t h2d = 0;
+        TwiddleSet* t = nullptr;
+        if (ensure_twiddles(c, n, &h2d, &t)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (ntt_fp2_rows(c, static_cast<const uint64_t*>(in), rows, n, static_cast<uint64_t*>(out), t->fwd))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_NTT, h2d, 0);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Host-pointer NTTs (staged through workspaces; synchronous)
+// ---------------------------------------------------------------------------
+
+namespace {
+int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size_t n, uint64_t* out) {
+    size_t total = 0, bytes = 0, in_bytes = 0;
+    if (!mul_ok(rows, n, &total) || !mul_ok(total, 8, &bytes) || !mul_ok(rows * msg_len, 8, &in_bytes))
+        return fail_msg(c, "Fp NTT geometry overflows size_t");
+    if (ensure_ws(c, WS_IN, std::max<size_t>(in_bytes, 8)) || ensure_ws(c, WS_OUT, bytes)) return -1;
+    uint64_t h2d = 0;
+    TwiddleSet* t = nullptr;
+    if (ensure_twiddles(c, n, &h2d, &t)) return -1;
+    if (begin_op(c)) return -1;
+    // Compact rows cross PCIe once; zero padding happens in the kernel load.
+    if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<uint64_t>(c, WS_IN), msgs, in_bytes, hipMemcpyHostToDevice, c->stream));
+    h2d += in_bytes;
+    if (mark_op(c, 1)) return -1;
+    if (ntt_fp_rows(c, ws<uint64_t>(c, WS_IN), msg_len, msg_len, rows, n, ws<uint64_t>(c, WS_OUT), t->fwd, false))
+        return -1;
+    if (mark_op(c, 2)) return -1;
+    VMX_HIP(c, hipMemcpyAsync(out, ws<uint64_t>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
+    return finish_op(c, OP_PCS_NTT, h2d, bytes);
+}
+}  // namespace
+
+// Replaces volta_cuda_ntt_fp (.cu:5534-5544).
+VMX_API int volta_cuda_ntt_fp(void* raw, const uint64_t* msg, size_t msg_len, size_t n, uint64_t* out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !msg || !out || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT geometry");
+    return guarded(c, "Fp NTT", [&] { return host_ntt(c, msg, 1, msg_len, n, out); });
+}
+
+// Replaces volta_cuda_ntt_fp_batch (.cu:5546-5559): compact rows of msg_len.
+VMX_API int volta_cuda_ntt_fp_batch(void* raw, const uint64_t* msgs, size_t rows, size_t msg_len, size_t n,
+                                       uint64_t* out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !msgs || !out || !rows || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT batch geometry");
+    return guarded(c, "Fp NTT batch", [&] { return host_ntt(c, msgs, rows, msg_len, n, out); });
+}
+
+// Replaces volta_cuda_ntt_fp2 (.cu:5561-5571).
+VMX_API int volta_cuda_ntt_fp2(void* raw, const Fp2* msg, size_t msg_len, size_t n, Fp2* out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !msg || !out || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp2 NTT geometry");
+    return guarded(c, "Fp2 NTT", [&] {
+        const size_t bytes = n * sizeof(Fp2), in_bytes = msg_len * sizeof(Fp2);
+        if (ensure_ws(c, WS_IN, bytes) || ensure_ws(c, WS_OUT, bytes)) return -1;
+        uint64_t h2d = 0;
+        TwiddleSet* t = nullptr;
+        if (ensure_twiddles(c, n, &h2d, &t)) return -1;
+        if (begin_op(c)) return -1;
+        if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), msg, in_bytes, hipMemcpyHostToDevice, c->stream));
+        if (bytes > in_bytes && zero_bytes(c, ws<unsigned char>(c, WS_IN) + in_bytes, bytes - in_bytes)) return -1;
+        h2d += bytes;
+        if (mark_op(c, 1)) return -1;
+        if (ntt_fp2_rows(c, ws<uint64_t>(c, WS_IN), 1, n, ws<uint64_t>(c, WS_OUT), t->fwd)) return -1;
+        if (mark_op(c, 2)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(out, ws<Fp2>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
+        return finish_op(c, OP_PCS_NTT, h2d, bytes);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// PCS rows
+// ---------------------------------------------------------------------------
+
+// Replaces volta_cuda_pcs_messages_device (.cu:7064-7079): msg = lift(w) || pads || 0.
+VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_off, uint64_t pads_id,
+                                              size_t pads_off, size_t rows, size_t cols, size_t pad, size_t code_len,
+                                              uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !code_len || cols + pad > code_len || cols + pad < cols)
+        return fail_msg(c, "invalid resident PCS message geometry");
+    return guarded(c, "resident PCS messages", [&] {
+        size_t wn = 0, pn = 0, on = 0;
+        if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(rows, code_len, &on))
+            return fail_msg(c, "resident PCS message geometry overflows size_t");
+        void *w = nullptr, *pads = nullptr, *out = nullptr;
+        if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
+            region_elems(c, out_id, out_off, on, 8, &out))
+            return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols, pad,
+                         code_len, static_cast<uint64_t*>(out)))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}
+
+namespace {
+int combine_device(Context* c, uint64_t w_id, size_t w_off, uint64_t pads_id, size_t pads_off, uint64_t co_id,
+                   size_t co_off, size_t rows, size_t cols, size_t pad, size_t combinations, uint64_t out_id,
+                   size_t out_off) {
+    size_t wn = 0, pn = 0, cn = 0, msg_len = 0, on = 0;
+    if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(combinations, rows, &cn) ||
+        !add_ok(cols, pad, &msg_len) || !mul_ok(combinations, msg_len, &on))
+        return fail_msg(c, "resident PCS combination geometry overflows size_t");
+    void *w = nullptr, *pads = nullptr, *co = nullptr, *out = nullptr;
+    if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
+        region_elems(c, co_id, co_off, cn, 16, &co) || region_elems(c, out_id, out_off, on, 16, &out))
+        return -1;
+    if (begin_op(c) || mark_op(c, 1)) return -1;
+    if (pcs_combine_rows(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
+                         static_cast<const Fp2*>(co), rows, cols, pad, combinations, static_cast<Fp2*>(out)))
+        return -1;
+    if (mark_op(c, 2)) return -1;
+    return finish_op(c, OP_PCS_ROWS, 0, 0);
+}
+}  // namespace
+
+// Replaces volta_cuda_pcs_combine_rows_device (.cu:7081-7099).
+VMX_API int volta_cuda_pcs_combine_rows_device(void* raw, uint64_t w_id, size_t w_off, uint64_t pads_id,
+                                                  size_t pads_off, uint64_t co_id, size_t co_off, size_t rows,
+                                                  size_t cols, size_t pad, size_t combinations, uint64_t out_id,
+                                                  size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !combinations) return fail_msg(c, "invalid resident PCS combination geometry");
+    return guarded(c, "resident PCS combination", [&] {
+        return combine_device(c, w_id, w_off, pads_id, pads_off, co_id, co_off, rows, cols, pad, combinations,
+                              out_id, out_off);
+    });
+}
+
+// Replaces volta_cuda_pcs_combine_rows (.cu:7228-7241): host buffers in/out.
+VMX_API int volta_cuda_pcs_combine_rows(void* raw, const int16_t* weights, const uint64_t* pads, const Fp2* coeffs,
+                                           size_t rows, size_t cols, size_t pad, size_t combinations, Fp2* out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !weights || !coeffs || !out || !rows || !cols || !combinations || (pad && !pads))
+        return fail_msg(c, "invalid PCS row-combination geometry");
+    return guarded(c, "PCS row combination", [&] {
+        size_t wb = 0, pb = 0, cb = 0, ob = 0;
+        if (!mul_ok(rows * cols, 2, &wb) || !mul_ok(rows * pad, 8, &pb) || !mul_ok(combinations * rows, 16, &cb) ||
+            !mul_ok(combinations * (cols + pad), 16, &ob))
+            return fail_msg(c, "PCS row-combination geometry overflows size_t");
+        if (ensure_ws(c, WS_IN, wb) || ensure_ws(c, WS_AUX0, std::max<size_t>(pb, 8)) || ensure_ws(c, WS_AUX1, cb) ||
+            ensure_ws(c, WS_OUT, ob))
+            return -1;
+        if (begin_op(c)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), weights, wb, hipMemcpyHostToDevice, c->stream));
+        if (pb) VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), pads, pb, hipMemcpyHostToDevice, c->stream));
+        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX1), coeffs, cb, hipMemcpyHostToDevice, c->stream));
+        if (mark_op(c, 1)) return -1;
+        if (pcs_combine_rows(c, ws<int16_t>(c, WS_IN), ws<uint64_t>(c, WS_AUX0), ws<Fp2>(c, WS_AUX1), rows, cols, pad,
+                             combinations, ws<Fp2>(c, WS_OUT)))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost, c->stream));
+        return finish_op(c, OP_PCS_ROWS, wb + pb + cb, ob);
+    });
+}
+
+// Replaces volta_cuda_fp2_powers_device (.cu:4107-4126): [c^1 .. c^count].
+VMX_API int volta_cuda_fp2_powers_device(void* raw, uint64_t c0, uint64_t c1, uint64_t out_id, size_t out_off,
+                                            size_t count) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !count || c0 >= gl::P || c1 >= gl::P) return fail_msg(c, "invalid Fp2 powers input");
+    return guarded(c, "Fp2 powers", [&] {
+        void* out = nullptr;
+        if (region_elems(c, out_id, out_off, count, 16, &out)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (fp2_powers(c, Fp2{c0, c1}, static_cast<Fp2*>(out), count)) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0, 0, 0, count * sizeof(Fp2));
+    });
+}
+
+// Replaces volta_cuda_fp2_add_inplace_device (.cu:7101-7112).
+VMX_API int volta_cuda_fp2_add_inplace_device(void* raw, uint64_t t_id, size_t t_off, uint64_t a_id, size_t a_off,
+                                                 size_t n) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !n) return fail_msg(c, "invalid resident Fp2 add");
+    return guarded(c, "resident Fp2 add", [&] {
+        void *t = nullptr, *a = nullptr;
+        if (region_elems(c, t_id, t_off, n, 16, &t) || region_elems(c, a_id, a_off, n, 16, &a)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (fp2_add_inplace(c, static_cast<Fp2*>(t), static_cast<const Fp2*>(a), n)) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}
+
+// Replaces volta_cuda_pcs_gather_columns_device (.cu:7243-7254).
+VMX_API int volta_cuda_pcs_gather_columns_device(void* raw, uint64_t m_id, size_t m_off, size_t rows, size_t cols,
+                                                    uint64_t idx_id, size_t idx_off, size_t queries, uint64_t out_id,
+                                                    size_t out_off, int fp2) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !queries) return fail_msg(c, "invalid resident PCS gather geometry");
+    return guarded(c, "resident PCS gather", [&] {
+        const size_t elem = fp2 ? 16 : 8;
+        size_t mn = 0, on = 0;
+        if (!mul_ok(rows, cols, &mn) || !mul_ok(rows, queries, &on))
+            return fail_msg(c, "resident PCS gather geometry overflows size_t");
+        void *m = nullptr, *idx = nullptr, *out = nullptr;
+        if (region_elems(c, m_id, m_off, mn, elem, &m) || region_elems(c, idx_id, idx_off, queries, 4, &idx) ||
+            region_elems(c, out_id, out_off, on, elem, &out))
+            return -1;
+        // Indices live on the device and are validated by the Rust seam before
+        // upload (rust/volta-accel/src/lib.rs:6773-6827); the kernel reads an
+        // out-of-range index as a zero column rather than faulting.
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (gather_columns(c, static_cast<const uint64_t*>(m), static_cast<const uint32_t*>(idx),
+                           static_cast<uint64_t*>(out), rows, cols, queries, fp2 != 0))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}
+
+// Replaces volta_cuda_pcs_gather_columns (.cu:7243-7254 host form).
+VMX_API int volta_cuda_pcs_gather_columns(void* raw, const uint64_t* matrix, size_t rows, size_t cols,
+                                             const uint32_t* idx, size_t queries, uint64_t* out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !matrix || !idx || !out || !rows || !cols || !queries)
+        return fail_msg(c, "invalid PCS column-gather geometry");
+    for (size_t q = 0; q < queries; ++q)
+        if (idx[q] >= cols) return fail_msg(c, "PCS column-gather index out of range");
+    return guarded(c, "PCS column gather", [&] {
+        size_t mb = 0, ob = 0;
+        if (!mul_ok(rows * cols, 8, &mb) || !mul_ok(rows * queries, 8, &ob))
+            return fail_msg(c, "PCS column-gather geometry overflows size_t");
+        const size_t ib = queries * 4;
+        if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_AUX0, ib) || ensure_ws(c, WS_OUT, ob)) return -1;
+        if (begin_op(c)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
+        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), idx, ib, hipMemcpyHostToDevice, c->stream));
+        if (mark_op(c, 1)) return -1;
+        if (gather_columns(c, ws<uint64_t>(c, WS_IN), ws<uint32_t>(c, WS_AUX0), ws<uint64_t>(c, WS_OUT), rows, cols,
+                           queries, false))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost, c->stream));
+        return finish_op(c, OP_PCS_ROWS, mb + ib, ob);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// ChaCha8 FpStream rows
+// ---------------------------------------------------------------------------
+
+namespace {
+constexpr uint64_t RESERVED_MOCK_BITS = (uint64_t{1} << 63) | (uint64_t{1} << 62) | (uint64_t{1} << 61);
+
+int fp_rows_impl(Context* c, uint64_t out_id, size_t out_off_bytes, const uint8_t* seed, uint64_t base, size_t rows,
+                 size_t count, int op) {
+    if (!c || !seed || !rows || !count) return fail_msg(c, "invalid ChaCha8 Fp row generation: rows and count must be non-zero");
+    if (rows - 1 > UINT64_MAX - base) return fail_msg(c, "ChaCha8 Fp row domain overflows u64");
+    const uint64_t last = base + static_cast<uint64_t>(rows - 1);
+    if (op == OP_AUTH_MASKS && ((base | last) & RESERVED_MOCK_BITS))
+        return fail_msg(c, "mock correlation mask domain sets reserved correlation bits");
+    size_t elems = 0, bytes = 0;
+    if (!mul_ok(rows, count, &elems) || !mul_ok(elems, 8, &bytes))
+        return fail_msg(c, "ChaCha8 Fp row geometry overflows size_t");
+    void* out = nullptr;
+    if (region(c, out_id, out_off_bytes, bytes, &out)) return -1;
+    if (begin_op(c) || mark_op(c, 1)) return -1;
+    if (chacha8_fp_rows(c, seed, base, rows, count, static_cast<uint64_t*>(out))) return -1;
+    if (mark_op(c, 2)) return -1;
+    return finish_op(c, op, 0, 0, 0, 0, bytes);
+}
+}  // namespace
+
+// Replaces volta_cuda_chacha8_prover_secret_fp_rows_device (.cu:3991-4047):
+// row r = FpStream::domain_separated(seed, base + r), `count` draws each.
+VMX_API int volta_cuda_chacha8_prover_secret_fp_rows_device(void* raw, uint64_t out_id, size_t out_off_bytes,
+                                                               const uint8_t* seed, uint64_t base, size_t rows,
+                                                               size_t count) {
+    Context* c = static_cast<Context*>(raw);
+    return guarded(c, "ChaCha8 Fp rows", [&] { return fp_rows_impl(c, out_id, out_off_bytes, seed, base, rows, count, OP_PCS_ROWS); });
+}
+
+// Replaces volta_cuda_mock_correlation_sub_masks_device (.cu:4049-4058).
+VMX_API int volta_cuda_mock_correlation_sub_masks_device(void* raw, uint64_t out_id, size_t out_off_bytes,
+                                                            const uint8_t* seed, uint64_t base, size_t rows,
+                                                            size_t cols) {
+    Context* c = static_cast<Context*>(raw);
+    return guarded(c, "mock correlation masks", [&] { return fp_rows_impl(c, out_id, out_off_bytes, seed, base, rows, cols, OP_AUTH_MASKS); });
+}
+
+// Replaces volta_cuda_chacha8_prover_secret_fp2_rows_padded_device (.cu:4060-4098).
+VMX_API int volta_cuda_chacha8_prover_secret_fp2_rows_padded_device(void* raw, uint64_t out_id,
+                                                                       size_t out_off_bytes, const uint8_t* seed,
+                                                                       uint64_t base, size_t rows, size_t count,
+                                                                       size_t padded) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !seed || !rows || !count || count > padded)
+        return fail_msg(c, "invalid prover-secret padded Fp2 row generation");
+    return guarded(c, "ChaCha8 Fp2 rows", [&] {
+        if (rows - 1 > UINT64_MAX - base) return fail_msg(c, "prover-secret Fp2 row domain overflows u64");
+        size_t out_elems = 0, out_bytes = 0, gen = 0, zero = 0;
+        if (!mul_ok(rows, padded, &out_elems) || !mul_ok(out_elems, 16, &out_bytes) || !mul_ok(rows * count, 16, &gen) ||
+            !mul_ok(rows * (padded - count), 16, &zero))
+            return fail_msg(c, "prover-secret Fp2 row geometry overflows size_t");
+        void* out = nullptr;
+        if (region(c, out_id, out_off_bytes, out_bytes, &out)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (chacha8_fp2_rows_padded(c, seed, base, rows, count, padded, static_cast<Fp2*>(out))) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0, 0, zero, gen);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// MI355X extensions (no counterpart in the reference ABI)
+// ---------------------------------------------------------------------------
+
+// Inverse NTT of pre-padded rows: a_i = n^-1 sum_j A_j w^-ij.  The reference
+// has no inverse transform; the large-transform configuration needs one.
+VMX_API int volta_mi355x_ntt_fp_inverse_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows,
+                                                        size_t n, uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident inverse Fp NTT geometry");
+    return guarded(c, "resident inverse Fp NTT", [&] {
+        size_t total = 0;
+        if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident inverse Fp NTT geometry overflows size_t");
+        void *in = nullptr, *out = nullptr;
+        if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
+            return -1;
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+            return fail_msg(c, "resident inverse Fp NTT input and output overlap");
+        return resident_ntt(c, static_cast<const uint64_t*>(in), n, n, rows, n, static_cast<uint64_t*>(out), true);
+    });
+}
+
+// RS-encode of compact resident u64 rows (msg_len per row) into rows x n
+// codewords, zero padding in the load: the resident form of the host
+// volta_cuda_ntt_fp_batch without a padded input copy in HBM.
+VMX_API int volta_mi355x_ntt_fp_encode_device(void* raw, uint64_t in_id, size_t in_off, size_t rows,
+                                                 size_t msg_len, size_t n, uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2(n) || msg_len > n) return fail_msg(c, "invalid resident Fp encode geometry");
+    return guarded(c, "resident Fp encode", [&] {
+        size_t in_n = 0, out_n = 0;
+        if (!mul_ok(rows, msg_len, &in_n) || !mul_ok(rows, n, &out_n))
+            return fail_msg(c, "resident Fp encode geometry overflows size_t");
+        void *in = nullptr, *out = nullptr;
+        if (region_elems(c, in_id, in_off, std::max<size_t>(in_n, 1), 8, &in) ||
+            region_elems(c, out_id, out_off, out_n, 8, &out))
+            return -1;
+        if (in_id == out_id) return fail_msg(c, "resident Fp encode input and output must be distinct buffers");
+        return resident_ntt(c, static_cast<const uint64_t*>(in), msg_len, msg_len, rows, n,
+                            static_cast<uint64_t*>(out), false);
+    });
+}
+
+// Fused Ligero encode: codeword rows NTT(lift(w) || pads || 0) straight from
+// the i16 weights, without the rows x code_len message buffer that
+// volta_cuda_pcs_messages_device + volta_cuda_ntt_fp_batch_device materialise.
+// Same result as that pair; stats: one PcsNtt call (+ the twiddle upload).
+VMX_API int volta_mi355x_pcs_encode_device(void* raw, uint64_t w_id, size_t w_off, uint64_t pads_id,
+                                              size_t pads_off, size_t rows, size_t cols, size_t pad, size_t code_len,
+                                              uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !pow2(code_len) || cols + pad > code_len || cols + pad < cols)
+        return fail_msg(c, "invalid resident PCS encode geometry");
+    return guarded(c, "resident PCS encode", [&] {
+        size_t wn = 0, pn = 0, on = 0;
+        if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(rows, code_len, &on))
+            return fail_msg(c, "resident PCS encode geometry overflows size_t");
+        void *w = nullptr, *pads = nullptr, *out = nullptr;
+        if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
+            region_elems(c, out_id, out_off, on, 8, &out))
+            return -1;
+        uint64_t h2d = 0;
+        TwiddleSet* t = nullptr;
+        if (ensure_twiddles(c, code_len, &h2d, &t)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        int rc = 1;
+        if (pad == 0)
+            rc = encode_i16_fast(c, static_cast<const int16_t*>(w), rows, cols, code_len, static_cast<uint64_t*>(out),
+                                 t->fwd);
+        if (rc < 0) return -1;
+        if (rc == 1 && ntt_msg_i16_rows(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows,
+                                        cols, pad, code_len, static_cast<uint64_t*>(out), t->fwd))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_NTT, h2d, 0);
+    });
+}
+
+// Row combination over dense resident u64 (Fp) rows: out[comb][j] =
+// sum_i coeffs[comb*rows + i] * m[i*cols + j].  The reference ABI only combines
+// i16 message rows; its own arithmetic benchmark combines u64 rows
+// (cuda/p7_pcs_arithmetic.cu:275-288).
+VMX_API int volta_mi355x_combine_rows_fp_device(void* raw, uint64_t m_id, size_t m_off, size_t rows, size_t cols,
+                                                   uint64_t co_id, size_t co_off, size_t combinations,
+                                                   uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !combinations) return fail_msg(c, "invalid resident Fp combination geometry");
+    return guarded(c, "resident Fp combination", [&] {
+        size_t mn = 0, cn = 0, on = 0;
+        if (!mul_ok(rows, cols, &mn) || !mul_ok(combinations, rows, &cn) || !mul_ok(combinations, cols, &on))
+            return fail_msg(c, "resident Fp combination geometry overflows size_t");
+        void *m = nullptr, *co = nullptr, *out = nullptr;
+        if (region_elems(c, m_id, m_off, mn, 8, &m) || region_elems(c, co_id, co_off, cn, 16, &co) ||
+            region_elems(c, out_id, out_off, on, 16, &out))
+            return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (combine_rows_fp(c, static_cast<const uint64_t*>(m), rows, cols, static_cast<const Fp2*>(co), combinations,
+                            static_cast<Fp2*>(out)))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}
+
+// Raw device address of a resident region, for measurement harnesses that
+// time kernels with their own events on the context stream.
+VMX_API int volta_mi355x_resident_device_ptr(void* raw, uint64_t id, size_t off_bytes, size_t bytes, void** out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !out) return fail_msg(c, "invalid device-pointer query");
+    return region(c, id, off_bytes, bytes, out);
+}
+
+// The context's HIP stream (hipStream_t), for event timing by a harness.
+VMX_API int volta_mi355x_stream(void* raw, void** out) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !out) return fail_msg(c, "invalid stream query");
+    *out = c->stream;
+    return 0;
+}
+
+// Measurement probes: streaming copy (achievable HBM bandwidth) and the
+// reference's Fp2-multiply stream/chain roofline kernels.
+VMX_API int volta_mi355x_probe_copy_device(void* raw, uint64_t src_id, uint64_t dst_id, size_t bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !bytes || bytes % 16) return fail_msg(c, "invalid copy probe geometry (bytes must be a multiple of 16)");
+    void *s = nullptr, *d = nullptr;
+    if (region(c, src_id, 0, bytes, &s) || region(c, dst_id, 0, bytes, &d)) return -1;
+    return probe_copy(c, s, d, bytes);
+}
+
+VMX_API int volta_mi355x_probe_fp2_device(void* raw, uint64_t a_id, uint64_t b_id, uint64_t out_id, size_t n,
+                                             int rounds) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !n || rounds < 0) return fail_msg(c, "invalid Fp2 probe geometry");
+    void *a = nullptr, *b = nullptr, *o = nullptr;
+    if (region_elems(c, a_id, 0, n, 16, &a) || region_elems(c, b_id, 0, n, 16, &b) ||
+        region_elems(c, out_id, 0, n, 16, &o))
+        return -1;
+    if (rounds == 0)
+        return probe_fp2_stream(c, static_cast<const Fp2*>(a), static_cast<const Fp2*>(b), static_cast<Fp2*>(o), n);
+    return probe_fp2_chain(c, static_cast<const Fp2*>(a), static_cast<const Fp2*>(b), static_cast<Fp2*>(o), n, rounds);
+}
+
+VMX_API int volta_mi355x_synchronize(void* raw) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c) return -1;
+    return sync_stream(c, SyncReason::HostOutput);
+}

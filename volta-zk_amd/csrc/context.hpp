@@ -1,0 +1,269 @@
+// context.hpp -- per-context state behind the volta_cuda_* C ABI (ABI 37).
+//
+// One context = one HIP stream on the current device, a generational-id
+// resident allocator with best-fit reuse of freed storage, a handful of
+// grow-only workspaces for the host-pointer entry points, a per-size twiddle
+// cache, and RawStats accounting/timing.  The observable contract follows the
+// reference backend (cuda/volta_cuda_backend.cu:55-123 RawStats layout,
+// :174-310 ids and buffers, :1035-1262 timing, :3150-3560 control exports).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <array>
+#include <chrono>
+#include <cstddef>
+#include <map>
+#include <string>
+#include <vector>
+
+// Exported C entry point (the library is built with hidden visibility).
+#define VMX_API extern "C" __attribute__((visibility("default")))
+
+namespace vmx {
+
+constexpr uint32_t ABI_VERSION = 37;
+constexpr int OP_COUNT = 7;
+constexpr int OP_GEMM = 0;
+constexpr int OP_LOGUP = 1;
+constexpr int OP_PCS_ROWS = 2;
+constexpr int OP_PCS_NTT = 3;
+constexpr int OP_PCS_MERKLE = 4;
+constexpr int OP_AUTH_MASKS = 5;
+constexpr int OP_MAILBOX = 6;
+
+// Timing modes reported in RawStats::timing_mode (reference .cu:42-46).
+constexpr uint32_t TIMING_EVENTS = 1;           // per-primitive events, read at once
+constexpr uint32_t TIMING_HOST_BARRIER_WALL = 2; // events unusable: host barriers
+constexpr uint32_t TIMING_EVENTS_DEFERRED = 3;  // events resolved lazily from a ring
+constexpr uint32_t TIMING_WALL_ONLY_COUNTERS = 4; // counters only, no events
+constexpr size_t TIMING_RING_SIZE = 512;
+
+// Exact field order of the reference's RawStats (504 bytes).
+struct RawStats {
+    uint64_t calls[OP_COUNT];
+    uint64_t kernel_ns[OP_COUNT];
+    uint64_t h2d_bytes;
+    uint64_t d2h_bytes;
+    uint64_t d2d_bytes;
+    uint64_t device_zeroed_bytes;
+    uint64_t device_generated_bytes;
+    uint64_t h2d_ns;
+    uint64_t d2h_ns;
+    uint64_t resident_h2d_host_calls;
+    uint64_t resident_d2h_host_calls;
+    uint64_t resident_h2d_host_call_ns;
+    uint64_t resident_d2h_host_call_ns;
+    uint64_t synchronizations;
+    uint64_t synchronization_ns;
+    uint64_t sync_host_output;
+    uint64_t sync_upload_lifetime;
+    uint64_t sync_timing_flush;
+    uint64_t sync_profiling_legacy;
+    uint64_t sync_allocator_flush;
+    uint64_t allocation_calls;
+    uint64_t resident_alloc_requests;
+    uint64_t resident_reuse_hits;
+    uint64_t resident_free_requests;
+    uint64_t physical_free_calls;
+    uint64_t live_device_bytes;
+    uint64_t peak_device_bytes;
+    uint64_t pinned_allocation_calls;
+    uint64_t pinned_alloc_requests;
+    uint64_t pinned_reuse_hits;
+    uint64_t pinned_free_requests;
+    uint64_t pinned_physical_free_calls;
+    uint64_t pinned_host_write_calls;
+    uint64_t pinned_host_write_bytes;
+    uint64_t live_pinned_bytes;
+    uint64_t peak_pinned_bytes;
+    uint64_t x4c_arena_reset_calls;
+    uint64_t x4c_arena_reset_bytes;
+    uint64_t x4c_kernel_launches;
+    uint64_t x4c_control_peek_calls;
+    uint64_t x4c_control_peek_pending;
+    uint64_t timing_records;
+    uint64_t timing_elapsed_query_attempts;
+    uint64_t timing_elapsed_no_write;
+    uint64_t timing_event_queries;
+    uint64_t timing_event_api_calls;
+    uint64_t timing_pending_high_water;
+    uint64_t timing_flush_count;
+    uint64_t coarse_timing_scopes;
+    uint64_t coarse_timing_ns;
+    uint32_t timing_mode;
+    uint32_t reserved;
+};
+static_assert(sizeof(RawStats) == 504, "RawStats must keep the reference's 504-byte layout");
+
+struct RawPinnedMemoryStats {
+    uint64_t active_bytes;
+    uint64_t cached_bytes;
+    uint64_t active_allocations;
+    uint64_t cached_allocations;
+    uint64_t in_flight_allocations;
+    uint64_t physical_allocation_calls;
+    uint64_t allocation_requests;
+    uint64_t reuse_hits;
+    uint64_t free_requests;
+    uint64_t physical_free_calls;
+    uint64_t host_write_calls;
+    uint64_t host_write_bytes;
+    uint64_t peak_bytes;
+};
+static_assert(sizeof(RawPinnedMemoryStats) == 104, "pinned stats layout");
+
+struct RawX4cControlState {
+    uint32_t stream_state;
+    uint32_t flags;
+    uint64_t outstanding_cuda_operations;
+    uint64_t pending_timing_records;
+    uint64_t active_device_allocations;
+    uint64_t cached_device_allocations;
+    uint64_t active_pinned_allocations;
+    uint64_t cached_pinned_allocations;
+    uint64_t in_flight_pinned_allocations;
+    uint64_t workspace_device_bytes;
+    uint64_t active_device_bytes;
+    uint64_t cached_device_bytes;
+    uint64_t active_pinned_bytes;
+    uint64_t cached_pinned_bytes;
+};
+static_assert(sizeof(RawX4cControlState) == 104, "control-state layout");
+
+enum class SyncReason { HostOutput, UploadLifetime, TimingFlush, ProfilingLegacy, AllocatorFlush };
+
+// Resident storage addressed by id = (generation << 32) | (slot + 1).
+struct Resident {
+    void* ptr = nullptr;
+    size_t capacity = 0;
+    size_t logical = 0;
+    uint32_t generation = 0;
+    bool active = false;
+};
+
+struct Pinned {
+    void* ptr = nullptr;
+    size_t capacity = 0;
+    size_t logical = 0;
+    hipEvent_t ready = nullptr;
+    uint32_t generation = 0;
+    bool active = false;
+    bool in_flight = false;
+};
+
+struct Workspace {
+    void* ptr = nullptr;
+    size_t capacity = 0;
+};
+
+// Workspace slots used by host-pointer entry points and internal scratch.
+enum WorkspaceSlot : int {
+    WS_IN = 0,
+    WS_OUT = 1,
+    WS_AUX0 = 2,
+    WS_AUX1 = 3,
+    WS_PARTIALS = 4,  // combination partial sums
+    WS_TRANSPOSE = 5, // four-step intermediate
+    WS_COUNT = 8,
+};
+
+struct TimingRecord {
+    hipEvent_t ev[4]{};
+    int op = -1;
+    uint8_t mask = 0;  // which of ev[] were recorded
+    bool coarse = false;
+    bool transfer_h2d = false;
+    bool transfer_d2h = false;
+    uint64_t h2d = 0, d2h = 0, d2d = 0, zeroed = 0, generated = 0;
+};
+
+// Device twiddle tables for one transform size n (all tables are uploaded once
+// and cached for the life of the context).
+struct TwiddleSet {
+    uint64_t* fwd = nullptr;  // w^0 .. w^(n/2-1), the reference's table
+    uint64_t* inv = nullptr;  // w^0 .. w^-(n/2-1) (inverse transform only)
+    size_t n = 0;
+};
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t events[4]{};
+    std::vector<Resident> resident;
+    std::vector<size_t> free_slots;  // inactive slots (may hold storage)
+    std::vector<Pinned> pinned;
+    std::vector<size_t> free_pinned;
+    Workspace ws[WS_COUNT];
+    std::map<size_t, TwiddleSet> twiddles;
+    RawStats stats{};
+    uint32_t timing_mode = TIMING_EVENTS;
+    // deferred ring
+    std::array<TimingRecord, TIMING_RING_SIZE> ring{};
+    size_t ring_begin = 0;
+    size_t ring_pending = 0;
+    bool record_active = false;  // a ring/legacy record is between begin and finish
+    size_t active_slot = 0;
+    // coarse scopes
+    bool coarse_active = false;
+    bool coarse_inner = false;
+    bool coarse_accounted = false;
+    bool poisoned = false;
+    int coarse_op = -1;
+    size_t coarse_slot = 0;
+    // counters-only
+    bool counter_active = false;
+    bool counter_pending = false;
+    uint64_t outstanding = 0;
+    std::chrono::steady_clock::time_point phase_start{};
+    uint64_t phase_ns[3]{};
+    uint32_t inject_no_write = 0;
+    std::string error;
+};
+
+// ---- error helpers (never throw across the ABI) -----------------------------
+int fail_msg(Context* c, const char* msg) noexcept;
+int fail_hip(Context* c, const char* what, hipError_t e) noexcept;
+int reject(Context* c, const char* msg) noexcept;
+
+#define VMX_HIP(c, call)                                              \
+    do {                                                              \
+        hipError_t vmx_e_ = (call);                                   \
+        if (vmx_e_ != hipSuccess) return ::vmx::fail_hip((c), #call, vmx_e_); \
+    } while (0)
+
+// ---- geometry helpers -----------------------------------------------------------
+bool mul_ok(size_t a, size_t b, size_t* out);
+bool add_ok(size_t a, size_t b, size_t* out);
+Resident* find_resident(Context* c, uint64_t id);
+// Resolve a byte region of a resident buffer; fails if out of bounds.
+int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out);
+// Element-offset variant: offset and count in units of elem_bytes.
+int region_elems(Context* c, uint64_t id, size_t offset, size_t count, size_t elem_bytes,
+                 void** out);
+int strided_region(Context* c, uint64_t id, size_t offset, size_t stride, size_t row_bytes,
+                   size_t rows, void** out, size_t* span);
+
+// ---- workspaces and twiddles ---------------------------------------------------
+int ensure_ws(Context* c, int slot, size_t bytes);
+template <typename T>
+T* ws(Context* c, int slot) {
+    return static_cast<T*>(c->ws[slot].ptr);
+}
+// Forward twiddles for size n; uploads n/2 u64 on first use and adds the
+// bytes to *h2d (the reference's per-size upload, .cu:2675-2689).
+int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
+int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
+
+// ---- timing/accounting (one primitive = begin, [mark1], [mark2], finish) ---------
+int begin_op(Context* c);
+int mark_op(Context* c, int which);
+int finish_op(Context* c, int op, uint64_t h2d, uint64_t d2h, uint64_t d2d = 0,
+              uint64_t zeroed = 0, uint64_t generated = 0);
+int begin_transfer(Context* c);
+int finish_transfer(Context* c, size_t bytes, bool h2d);
+int sync_stream(Context* c, SyncReason reason);
+int flush_deferred(Context* c, SyncReason reason);
+
+}  // namespace vmx

@@ -1,0 +1,109 @@
+// gl64.hpp -- Goldilocks field arithmetic for gfx950 (device) and the host.
+//
+// p = 2^64 - 2^32 + 1.  Elements are u64; "canonical" means in [0, p).
+// The identities used are 2^64 = 2^32 - 1 = eps (mod p) and 2^96 = -1 (mod p),
+// the same ones the reference's field uses (rust/volta-field/src/lib.rs:89-103).
+//
+// The device multiply forms the 128-bit product from four 32x32->64 partial
+// products (v_mad_u64_u32 on gfx950) and folds the high half with the two
+// identities above; no MFMA, no 64-bit hardware multiply exists on the VALU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gl {
+
+constexpr uint64_t P = 0xFFFFFFFF00000001ull;
+constexpr uint64_t EPS = 0x00000000FFFFFFFFull;
+
+// ---- host/device scalar ops (canonical in, canonical out) ---------------
+
+__host__ __device__ __forceinline__ uint64_t canon(uint64_t x) { return x >= P ? x - P : x; }
+
+__host__ __device__ __forceinline__ uint64_t add(uint64_t a, uint64_t b) {
+    uint64_t r = a + b;
+    // A carry out of 2^64 is worth eps; with a, b < p the corrected value
+    // stays below 2^64.
+    r += (r < a) ? EPS : 0;
+    return r >= P ? r - P : r;
+}
+
+__host__ __device__ __forceinline__ uint64_t sub(uint64_t a, uint64_t b) {
+    uint64_t r = a - b;
+    // A borrow is worth -2^64 = -eps; with a, b < p the result stays >= 0.
+    return (a < b) ? r - EPS : r;
+}
+
+__host__ __device__ __forceinline__ uint64_t neg(uint64_t a) { return a ? P - a : 0; }
+
+// Fold a 128-bit value (hi:lo) to a canonical element.
+__host__ __device__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
+    const uint64_t hh = hi >> 32;
+    const uint64_t hl = hi & EPS;
+    uint64_t t = lo - hh;               // lo - hh*2^96
+    t -= (lo < hh) ? EPS : 0;           // borrow of 2^64 = eps
+    const uint64_t m = (hl << 32) - hl; // hl * eps < 2^64
+    uint64_t r = t + m;
+    r += (r < m) ? EPS : 0;             // carry of 2^64 = eps
+    return r >= P ? r - P : r;
+}
+
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ void mul_wide(uint64_t a, uint64_t b, uint64_t& lo, uint64_t& hi) {
+    lo = a * b;
+    hi = __umul64hi(a, b);
+}
+#else
+inline void mul_wide(uint64_t a, uint64_t b, uint64_t& lo, uint64_t& hi) {
+    const unsigned __int128 p = static_cast<unsigned __int128>(a) * b;
+    lo = static_cast<uint64_t>(p);
+    hi = static_cast<uint64_t>(p >> 64);
+}
+#endif
+
+__host__ __device__ __forceinline__ uint64_t mul(uint64_t a, uint64_t b) {
+    uint64_t lo, hi;
+    mul_wide(a, b, lo, hi);
+    return fold128(lo, hi);
+}
+
+inline uint64_t pow_host(uint64_t a, uint64_t e) {
+    uint64_t acc = 1;
+    while (e) {
+        if (e & 1) acc = mul(acc, a);
+        a = mul(a, a);
+        e >>= 1;
+    }
+    return acc;
+}
+
+inline uint64_t inv_host(uint64_t a) { return pow_host(a, P - 2); }
+
+// Primitive 2^bits-th root of unity 7^((p-1) >> bits): the generator and
+// 2-adicity of the reference's NTT (rust/volta-pcs/src/ntt.rs:9-12).
+inline uint64_t root_of_unity(unsigned bits) { return pow_host(7, (P - 1) >> bits); }
+
+// i16 -> field: non-negative values embed as-is, negatives as p - |x|
+// (rust/volta-field/src/lib.rs:32-40).
+__host__ __device__ __forceinline__ uint64_t from_i16(int16_t x) {
+    return x >= 0 ? static_cast<uint64_t>(x) : P - static_cast<uint64_t>(-static_cast<int32_t>(x));
+}
+
+// ---- quadratic extension Fp2 = Fp[phi]/(phi^2 - 7) -----------------------
+
+struct alignas(8) Fp2 {
+    uint64_t c0;
+    uint64_t c1;
+};
+
+__host__ __device__ __forceinline__ Fp2 fp2_add(Fp2 a, Fp2 b) { return Fp2{add(a.c0, b.c0), add(a.c1, b.c1)}; }
+
+__host__ __device__ __forceinline__ Fp2 fp2_mul(Fp2 a, Fp2 b) {
+    // (a0 + a1 phi)(b0 + b1 phi) = (a0 b0 + 7 a1 b1) + (a0 b1 + a1 b0) phi
+    return Fp2{add(mul(a.c0, b.c0), mul(7, mul(a.c1, b.c1))), add(mul(a.c0, b.c1), mul(a.c1, b.c0))};
+}
+
+__host__ __device__ __forceinline__ Fp2 fp2_mul_base(Fp2 a, uint64_t x) { return Fp2{mul(a.c0, x), mul(a.c1, x)}; }
+
+}  // namespace gl

@@ -1,0 +1,54 @@
+// kernels.hpp -- host-side launchers for the device kernels.  All launch on
+// the context stream and return 0 or a context error; the callers in
+// abi_pcs.cpp do geometry validation and stats accounting.
+#pragma once
+
+#include <stdint.h>
+
+#include <cstddef>
+
+#include "context.hpp"
+#include "gl64.hpp"
+
+namespace vmx {
+
+int zero_bytes(Context* c, void* dst, size_t bytes);
+
+// rows x n forward (or inverse-scaled) NTT of u64 rows: input row r is
+// in[r*in_stride .. +msg_len), zero beyond; output rows are n wide.
+int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
+                uint64_t* out, const uint64_t* tw, bool inverse_scale_n);
+// Componentwise NTT of rows x n Fp2 (u64 pairs) with base-field twiddles.
+int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const uint64_t* tw);
+// Fused PCS encode: messages lift(w) || pads || 0 transformed without
+// materialising the message rows.
+int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
+                     size_t n, uint64_t* out, const uint64_t* tw);
+// Fast path for the Ligero shapes (i16 messages with rate <= 1/2 and
+// n in [2^11, 2^14]); returns 1 when the shape is not covered.
+int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
+                    const uint64_t* tw);
+
+int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
+                 size_t code_len, uint64_t* out);
+// out[comb][j], j < cols+pad, over message rows lift(w) || pads.
+int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const gl::Fp2* coeffs, size_t rows,
+                     size_t cols, size_t pad, size_t combinations, gl::Fp2* out);
+// The same combination over dense u64 (Fp) rows.
+int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, const gl::Fp2* coeffs,
+                    size_t combinations, gl::Fp2* out);
+int fp2_powers(Context* c, gl::Fp2 base, gl::Fp2* out, size_t count);
+int fp2_add_inplace(Context* c, gl::Fp2* target, const gl::Fp2* add, size_t n);
+int gather_columns(Context* c, const uint64_t* m, const uint32_t* idx, uint64_t* out, size_t rows,
+                   size_t cols, size_t queries, bool fp2);
+int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
+                    uint64_t* out);
+int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows,
+                            size_t count, size_t padded, gl::Fp2* out);
+
+// Measurement probes.
+int probe_copy(Context* c, const void* src, void* dst, size_t bytes);
+int probe_fp2_stream(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n);
+int probe_fp2_chain(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n, int rounds);
+
+}  // namespace vmx

@@ -1,0 +1,313 @@
+// ntt.hip -- batched Goldilocks NTT kernels for gfx950.
+//
+// Semantics are the reference's NttPlan::forward (rust/volta-pcs/src/ntt.rs:36-61):
+// out[j] = sum_i a_i w^(ij), w = 7^((p-1)/n), natural-order output.  Field sums
+// are exact, so any factorisation of the DFT gives bit-identical results.
+//
+// Generic paths (any power-of-two n):
+//   * n <= 2^14: one workgroup per row, the whole row in LDS (<= 128 KiB of the
+//     160 KiB per CU), bit-reversed load then radix-2^2 DIT passes (two stages
+//     per LDS round trip).  One HBM read + one HBM write per element.
+//   * n  > 2^14: four-step split n = n1*n2.  Pass A: n1-point column DFTs of
+//     C adjacent columns per workgroup plus the w^(i2*k1) twiddle; pass B:
+//     n2-point row DFTs of R adjacent rows with a transposed, R-element
+//     coalesced store.  Two HBM round trips.
+// All twiddles come from the reference's table w^0..w^(n/2-1): a stage of
+// length L of any sub-transform uses tw[k * n/L], and w^e for e >= n/2 is
+// -tw[e - n/2].
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "context.hpp"
+#include "gl64.hpp"
+#include "kernels.hpp"
+
+namespace vmx {
+
+__device__ __forceinline__ uint32_t brev(uint32_t x, int bits) { return __brev(x) >> (32 - bits); }
+
+// w^e for 0 <= e < n from the half table.
+__device__ __forceinline__ uint64_t tw_pow(const uint64_t* tw, size_t e, size_t half) {
+    return e < half ? tw[e] : gl::neg(tw[e - half]);
+}
+
+// `count` independent DIT transforms of size 2^fbits stored back to back in s,
+// each already in bit-reversed order.  Twiddle for stage length L = 2^l,
+// position k: tw[k << (gbits - l)] where 2^gbits is the size the table was
+// built for (the sub-transform root is a power of the table root).
+__device__ void lds_dit(uint64_t* s, int count, int fbits, int gbits, const uint64_t* tw) {
+    const int T = blockDim.x;
+    const int tid = threadIdx.x;
+    const size_t m = size_t{1} << fbits;
+    const size_t total = m * count;
+    int l = 1;
+    if (fbits & 1) {
+        for (size_t b = tid; b < total / 2; b += T) {
+            const size_t i0 = 2 * b;
+            const uint64_t u = s[i0], v = s[i0 + 1];
+            s[i0] = gl::add(u, v);
+            s[i0 + 1] = gl::sub(u, v);
+        }
+        __syncthreads();
+        l = 2;
+    }
+    for (; l < fbits; l += 2) {
+        const size_t half = size_t{1} << (l - 1);
+        const size_t len = size_t{1} << l;
+        const int sh1 = gbits - l;
+        const int sh2 = gbits - l - 1;
+        const size_t quads_per = m >> 2;
+        for (size_t qq = tid; qq < total / 4; qq += T) {
+            const size_t c = qq / quads_per;
+            const size_t q = qq - c * quads_per;
+            const size_t group = q >> (l - 1);
+            const size_t k = q & (half - 1);
+            uint64_t* base = s + c * m + group * 2 * len + k;
+            const uint64_t a0 = base[0], a1 = base[half], a2 = base[len], a3 = base[len + half];
+            const uint64_t w1 = tw[k << sh1];
+            uint64_t t = gl::mul(a1, w1);
+            const uint64_t b0 = gl::add(a0, t), b1 = gl::sub(a0, t);
+            t = gl::mul(a3, w1);
+            const uint64_t b2 = gl::add(a2, t), b3 = gl::sub(a2, t);
+            const uint64_t w2 = tw[k << sh2];
+            const uint64_t w3 = tw[(k + half) << sh2];
+            t = gl::mul(b2, w2);
+            base[0] = gl::add(b0, t);
+            base[len] = gl::sub(b0, t);
+            t = gl::mul(b3, w3);
+            base[half] = gl::add(b1, t);
+            base[len + half] = gl::sub(b1, t);
+        }
+        __syncthreads();
+    }
+}
+
+// ---- input loaders ------------------------------------------------------------
+
+// Dense u64 rows of `stride` elements; positions >= msg_len read as zero.
+struct LoadU64 {
+    const uint64_t* src;
+    size_t stride;
+    size_t msg_len;
+    __device__ uint64_t operator()(size_t row, size_t j) const {
+        return j < msg_len ? src[row * stride + j] : 0;
+    }
+};
+
+// Strided u64 lanes of Fp2 rows (component comp of rows of n Fp2).
+struct LoadFp2Comp {
+    const uint64_t* src;  // Fp2 storage viewed as u64
+    size_t n;
+    int comp;
+    __device__ uint64_t operator()(size_t row, size_t j) const { return src[2 * (row * n + j) + comp]; }
+};
+
+// PCS message rows lift(w) || pads || 0 (reference pcs_messages_kernel,
+// cuda/volta_cuda_backend.cu:2950-2958), fused into the transform load.
+struct LoadMsgI16 {
+    const int16_t* w;
+    const uint64_t* pads;
+    size_t cols, pad;
+    __device__ uint64_t operator()(size_t row, size_t j) const {
+        if (j < cols) return gl::from_i16(w[row * cols + j]);
+        if (j < cols + pad) return pads[row * pad + (j - cols)];
+        return 0;
+    }
+};
+
+struct StoreU64 {
+    uint64_t* dst;
+    __device__ void operator()(size_t idx, uint64_t v) const { dst[idx] = v; }
+};
+
+struct StoreFp2Comp {
+    uint64_t* dst;
+    int comp;
+    __device__ void operator()(size_t idx, uint64_t v) const { dst[2 * idx + comp] = v; }
+};
+
+// ---- whole-row kernel (n <= 2^14) ----------------------------------------------
+
+template <class Load, class Store>
+__global__ __launch_bounds__(512) void ntt_row_lds(Load ld, Store st, int bits, const uint64_t* tw,
+                                                  uint64_t scale) {
+    extern __shared__ uint64_t s[];
+    const size_t n = size_t{1} << bits;
+    const size_t row = blockIdx.x;
+    for (size_t j = threadIdx.x; j < n; j += blockDim.x) s[brev(static_cast<uint32_t>(j), bits)] = ld(row, j);
+    __syncthreads();
+    lds_dit(s, 1, bits, bits, tw);
+    if (scale != 1) {
+        for (size_t j = threadIdx.x; j < n; j += blockDim.x) st(row * n + j, gl::mul(s[j], scale));
+    } else {
+        for (size_t j = threadIdx.x; j < n; j += blockDim.x) st(row * n + j, s[j]);
+    }
+}
+
+// ---- four-step passes ---------------------------------------------------------------
+
+// Pass A: for columns i2 in [cb*C, cb*C + C) of row `row`, the n1-point DFT over
+// i1 of x[n2*i1 + i2], times w^(i2*k1), stored at y[k1*n2 + i2].
+template <class Load>
+__global__ __launch_bounds__(512) void ntt4_pass_a(Load ld, uint64_t* y, int bits, int b1, int cbits,
+                                                  const uint64_t* tw) {
+    extern __shared__ uint64_t s[];
+    const size_t n = size_t{1} << bits;
+    const size_t n1 = size_t{1} << b1;
+    const size_t n2 = n >> b1;
+    const size_t C = size_t{1} << cbits;
+    const size_t blocks_per_row = n2 >> cbits;
+    const size_t row = blockIdx.x / blocks_per_row;
+    const size_t c0 = (blockIdx.x - row * blocks_per_row) << cbits;
+    for (size_t e = threadIdx.x; e < C * n1; e += blockDim.x) {
+        const size_t i1 = e >> cbits, c = e & (C - 1);
+        s[c * n1 + brev(static_cast<uint32_t>(i1), b1)] = ld(row, n2 * i1 + c0 + c);
+    }
+    __syncthreads();
+    lds_dit(s, static_cast<int>(C), b1, bits, tw);
+    const size_t half = n >> 1;
+    for (size_t e = threadIdx.x; e < C * n1; e += blockDim.x) {
+        const size_t k1 = e >> cbits, c = e & (C - 1);
+        const size_t i2 = c0 + c;
+        const uint64_t v = gl::mul(s[c * n1 + k1], tw_pow(tw, (i2 * k1) & (n - 1), half));
+        y[row * n + k1 * n2 + i2] = v;
+    }
+}
+
+// Pass B: for k1 in [rb*R, rb*R + R), the n2-point DFT over i2 of y[k1*n2 + i2],
+// stored at out[k1 + n1*k2] (times `scale`).
+template <class Store>
+__global__ __launch_bounds__(512) void ntt4_pass_b(const uint64_t* y, Store st, int bits, int b1, int rbits,
+                                                  const uint64_t* tw, uint64_t scale) {
+    extern __shared__ uint64_t s[];
+    const size_t n = size_t{1} << bits;
+    const size_t n1 = size_t{1} << b1;
+    const int b2 = bits - b1;
+    const size_t n2 = n >> b1;
+    const size_t R = size_t{1} << rbits;
+    const size_t blocks_per_row = n1 >> rbits;
+    const size_t row = blockIdx.x / blocks_per_row;
+    const size_t r0 = (blockIdx.x - row * blocks_per_row) << rbits;
+    for (size_t e = threadIdx.x; e < R * n2; e += blockDim.x) {
+        const size_t r = e >> b2, i2 = e & (n2 - 1);
+        s[r * n2 + brev(static_cast<uint32_t>(i2), b2)] = y[row * n + (r0 + r) * n2 + i2];
+    }
+    __syncthreads();
+    lds_dit(s, static_cast<int>(R), b2, bits, tw);
+    for (size_t e = threadIdx.x; e < R * n2; e += blockDim.x) {
+        const size_t k2 = e >> rbits, r = e & (R - 1);
+        uint64_t v = s[r * n2 + k2];
+        if (scale != 1) v = gl::mul(v, scale);
+        st(row * n + (r0 + r) + n1 * k2, v);
+    }
+}
+
+// ---- launchers -------------------------------------------------------------------------
+
+// Row-offset adjusters so a launch can start at row r0.
+static void shift_rows(LoadU64& l, StoreU64& s, size_t r0, size_t n) {
+    l.src += r0 * l.stride;
+    s.dst += r0 * n;
+}
+static void shift_rows(LoadMsgI16& l, StoreU64& s, size_t r0, size_t n) {
+    l.w += r0 * l.cols;
+    if (l.pad) l.pads += r0 * l.pad;
+    s.dst += r0 * n;
+}
+static void shift_rows(LoadFp2Comp& l, StoreFp2Comp& s, size_t r0, size_t n) {
+    l.src += 2 * r0 * l.n;
+    s.dst += 2 * r0 * n;
+}
+
+
+static int ilog2(size_t n) {
+    int b = 0;
+    while ((size_t{1} << b) < n) ++b;
+    return b;
+}
+
+constexpr int LDS_MAX_BITS = 14;           // 128 KiB of u64 per workgroup
+constexpr size_t LDS_MAX_WORDS = size_t{1} << LDS_MAX_BITS;
+
+template <class K>
+static hipError_t allow_lds(K kernel, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+}
+
+template <class Load, class Store>
+static int run_ntt(Context* c, Load ld, Store st, size_t rows, size_t n, const uint64_t* tw, uint64_t scale) {
+    const int bits = ilog2(n);
+    if (bits <= LDS_MAX_BITS) {
+        const size_t lds = n * sizeof(uint64_t);
+        const int threads = static_cast<int>(std::min<size_t>(512, std::max<size_t>(64, n / 4)));
+        auto k = ntt_row_lds<Load, Store>;
+        VMX_HIP(c, allow_lds(k, lds));
+        // Rows are independent; launch in slices that fit the 32-bit grid.
+        for (size_t r0 = 0; r0 < rows; r0 += 0x7FFFFFFF) {
+            const size_t cnt = std::min<size_t>(rows - r0, 0x7FFFFFFF);
+            Load l2 = ld;
+            Store s2 = st;
+            shift_rows(l2, s2, r0, n);
+            hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(cnt)), dim3(threads), lds, c->stream, l2, s2, bits,
+                               tw, scale);
+            VMX_HIP(c, hipGetLastError());
+        }
+        return 0;
+    }
+    // Four-step through the transpose workspace, a bounded number of rows at a time.
+    const int b1 = (bits + 1) / 2;
+    const int b2 = bits - b1;
+    if (b1 > LDS_MAX_BITS) return fail_msg(c, "NTT size exceeds the supported maximum of 2^28");
+    const int cbits = std::min(b2, LDS_MAX_BITS - b1);
+    const int rbits = std::min(b1, LDS_MAX_BITS - b2);
+    const size_t row_bytes = n * sizeof(uint64_t);
+    const size_t max_ws = size_t{1} << 31;  // 2 GiB of intermediate at most
+    const size_t chunk = std::max<size_t>(1, std::min(rows, max_ws / row_bytes));
+    if (ensure_ws(c, WS_TRANSPOSE, chunk * row_bytes)) return -1;
+    uint64_t* y = ws<uint64_t>(c, WS_TRANSPOSE);
+    auto ka = ntt4_pass_a<Load>;
+    auto kb = ntt4_pass_b<Store>;
+    const size_t lds_a = (size_t{1} << (b1 + cbits)) * sizeof(uint64_t);
+    const size_t lds_b = (size_t{1} << (b2 + rbits)) * sizeof(uint64_t);
+    VMX_HIP(c, allow_lds(ka, lds_a));
+    VMX_HIP(c, allow_lds(kb, lds_b));
+    const size_t blocks_a = size_t{1} << (b2 - cbits);
+    const size_t blocks_b = size_t{1} << (b1 - rbits);
+    const int ta = static_cast<int>(std::min<size_t>(512, std::max<size_t>(64, (size_t{1} << (b1 + cbits)) / 4)));
+    const int tb = static_cast<int>(std::min<size_t>(512, std::max<size_t>(64, (size_t{1} << (b2 + rbits)) / 4)));
+    for (size_t r0 = 0; r0 < rows; r0 += chunk) {
+        const size_t cnt = std::min(chunk, rows - r0);
+        Load l2 = ld;
+        Store s2 = st;
+        shift_rows(l2, s2, r0, n);
+        hipLaunchKernelGGL(ka, dim3(static_cast<unsigned>(cnt * blocks_a)), dim3(ta), lds_a, c->stream, l2, y,
+                           bits, b1, cbits, tw);
+        VMX_HIP(c, hipGetLastError());
+        hipLaunchKernelGGL(kb, dim3(static_cast<unsigned>(cnt * blocks_b)), dim3(tb), lds_b, c->stream,
+                           static_cast<const uint64_t*>(y), s2, bits, b1, rbits, tw, scale);
+        VMX_HIP(c, hipGetLastError());
+    }
+    return 0;
+}
+
+int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
+                uint64_t* out, const uint64_t* tw, bool inverse_scale_n) {
+    const uint64_t scale = inverse_scale_n ? gl::inv_host(gl::canon(n)) : 1;
+    return run_ntt(c, LoadU64{in, in_stride, msg_len}, StoreU64{out}, rows, n, tw, scale);
+}
+
+int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const uint64_t* tw) {
+    for (int comp = 0; comp < 2; ++comp)
+        if (run_ntt(c, LoadFp2Comp{in, n, comp}, StoreFp2Comp{out, comp}, rows, n, tw, 1)) return -1;
+    return 0;
+}
+
+int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
+                     size_t n, uint64_t* out, const uint64_t* tw) {
+    return run_ntt(c, LoadMsgI16{w, pads, cols, pad}, StoreU64{out}, rows, n, tw, 1);
+}
+
+}  // namespace vmx

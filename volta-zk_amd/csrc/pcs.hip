@@ -1,0 +1,452 @@
+// pcs.hip -- PCS row kernels for gfx950: message rows, row combinations,
+// column gathers, Fp2 powers/adds, ChaCha8 FpStream rows, measurement probes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "chacha8.hpp"
+#include "context.hpp"
+#include "gl64.hpp"
+#include "kernels.hpp"
+
+namespace vmx {
+
+using gl::Fp2;
+
+static unsigned grid_for(size_t items, size_t per_block, size_t cap = 1u << 20) {
+    const size_t g = (items + per_block - 1) / per_block;
+    return static_cast<unsigned>(std::max<size_t>(1, std::min(g, cap)));
+}
+
+// ---- message rows (reference pcs_messages_kernel, .cu:2950-2958) --------------------
+
+__global__ void messages_kernel(const int16_t* w, const uint64_t* pads, uint64_t* out, size_t rows, size_t cols,
+                                size_t pad, size_t code_len) {
+    const size_t total = rows * code_len;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < total; z += stride) {
+        const size_t r = z / code_len, j = z - r * code_len;
+        uint64_t v = 0;
+        if (j < cols) v = gl::from_i16(w[r * cols + j]);
+        else if (j < cols + pad) v = pads[r * pad + (j - cols)];
+        out[z] = v;
+    }
+}
+
+int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
+                 size_t code_len, uint64_t* out) {
+    hipLaunchKernelGGL(messages_kernel, dim3(grid_for(rows * code_len, 256)), dim3(256), 0, c->stream, w, pads,
+                       out, rows, cols, pad, code_len);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// ---- row combinations ---------------------------------------------------------------------
+//
+// out[comb][j] = sum_i coeff[comb][i] * msg_i[j] (reference combine_row_range,
+// rust/volta-pcs/src/ligero.rs:1114-1135; coefficient layout combinations x
+// rows, rust/volta-accel/src/lib.rs:6522-6569).  Unlike the reference kernel,
+// which re-reads the matrix once per (combination, column) thread, the matrix
+// is read once: each workgroup owns a chunk of rows x a tile of columns,
+// accumulates all combinations lazily, and writes one partial per chunk; a
+// second kernel sums partials mod p.
+//
+// i16 data: with w' = w + 2^15 in [0, 2^16) and a coefficient component
+// x = xh*2^32 + xl, sum_i x_i w_i = sum xl_i w'_i + 2^32 sum xh_i w'_i
+// - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
+// absorb up to 2^16 rows exactly; the fold to a field element happens once.
+
+constexpr int COMB_COLS = 4;      // columns per thread (one 8-byte i16 load)
+constexpr int COMB_THREADS = 256;
+constexpr size_t COMB_CHUNK = 128; // rows per partial
+
+template <int KC>
+__global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_t* w, const Fp2* coeffs,
+                                                                   Fp2* partials, size_t rows, size_t cols,
+                                                                   size_t msg_len, size_t comb0,
+                                                                   size_t combinations, size_t chunk,
+                                                                   int vec_ok) {
+    const size_t j0 = (static_cast<size_t>(blockIdx.x) * COMB_THREADS + threadIdx.x) * COMB_COLS;
+    const size_t ck = blockIdx.y;
+    const size_t r0 = ck * chunk;
+    const size_t r1 = min(rows, r0 + chunk);
+    uint64_t acc_lo[KC][2][COMB_COLS] = {};
+    uint64_t acc_hi[KC][2][COMB_COLS] = {};
+    uint64_t s_lo[KC][2] = {}, s_hi[KC][2] = {};
+    const bool full = j0 + COMB_COLS <= cols;
+    for (size_t i = r0; i < r1; ++i) {
+        uint32_t wp[COMB_COLS];
+        if (full && vec_ok) {
+            const uint2 raw = *reinterpret_cast<const uint2*>(w + i * cols + j0);
+            wp[0] = (raw.x & 0xFFFFu) ^ 0x8000u;
+            wp[1] = (raw.x >> 16) ^ 0x8000u;
+            wp[2] = (raw.y & 0xFFFFu) ^ 0x8000u;
+            wp[3] = (raw.y >> 16) ^ 0x8000u;
+        } else {
+#pragma unroll
+            for (int q = 0; q < COMB_COLS; ++q) {
+                const size_t j = j0 + q;
+                wp[q] = j < cols ? (static_cast<uint32_t>(static_cast<uint16_t>(w[i * cols + j])) ^ 0x8000u) : 0x8000u;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            const Fp2 cf = coeffs[(comb0 + k) * rows + i];
+            const uint64_t comp[2] = {cf.c0, cf.c1};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t xl = static_cast<uint32_t>(comp[h]);
+                const uint32_t xh = static_cast<uint32_t>(comp[h] >> 32);
+                s_lo[k][h] += xl;
+                s_hi[k][h] += xh;
+#pragma unroll
+                for (int q = 0; q < COMB_COLS; ++q) {
+                    acc_lo[k][h][q] += static_cast<uint64_t>(xl) * wp[q];
+                    acc_hi[k][h][q] += static_cast<uint64_t>(xh) * wp[q];
+                }
+            }
+        }
+    }
+    const uint64_t two32 = 0x100000000ull;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+        if (comb0 + k >= combinations) break;
+        uint64_t bias[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // 2^15 * sum x_i  (mod p)
+            const uint64_t sx = gl::add(gl::canon(s_lo[k][h]), gl::mul(gl::canon(s_hi[k][h]), two32));
+            bias[h] = gl::mul(sx, 0x8000ull);
+        }
+#pragma unroll
+        for (int q = 0; q < COMB_COLS; ++q) {
+            const size_t j = j0 + q;
+            if (j >= cols) break;
+            uint64_t v[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint64_t t = gl::add(gl::canon(acc_lo[k][h][q]), gl::mul(gl::canon(acc_hi[k][h][q]), two32));
+                v[h] = gl::sub(t, bias[h]);
+            }
+            partials[(ck * combinations + comb0 + k) * msg_len + j] = Fp2{v[0], v[1]};
+        }
+    }
+}
+
+// Pad columns j in [cols, cols+pad): full field products.
+__global__ void combine_pads_partial(const uint64_t* pads, const Fp2* coeffs, Fp2* partials, size_t rows,
+                                     size_t cols, size_t pad, size_t msg_len, size_t combinations, size_t chunk) {
+    const size_t p = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const size_t comb = blockIdx.z;
+    if (p >= pad) return;
+    const size_t ck = blockIdx.y;
+    const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
+    Fp2 acc{0, 0};
+    for (size_t i = r0; i < r1; ++i) acc = gl::fp2_add(acc, gl::fp2_mul_base(coeffs[comb * rows + i], pads[i * pad + p]));
+    partials[(ck * combinations + comb) * msg_len + cols + p] = acc;
+}
+
+// Dense u64 rows: 128-bit products accumulated in three 64-bit limbs, folded
+// once per chunk (2^128 = -2^32 mod p).
+__device__ __forceinline__ uint64_t fold192(uint64_t lo, uint64_t hi, uint64_t top) {
+    const uint64_t base = gl::fold128(lo, hi);
+    // 2^128 = eps^2 = -2^32 (mod p)
+    return gl::sub(base, gl::mul(gl::canon(top), 0x100000000ull));
+}
+
+constexpr int FP_COLS = 2;
+
+template <int KC>
+__global__ __launch_bounds__(COMB_THREADS) void combine_fp_partial(const uint64_t* m, const Fp2* coeffs,
+                                                                  Fp2* partials, size_t rows, size_t cols,
+                                                                  size_t comb0, size_t combinations,
+                                                                  size_t chunk) {
+    const size_t j0 = (static_cast<size_t>(blockIdx.x) * COMB_THREADS + threadIdx.x) * FP_COLS;
+    const size_t ck = blockIdx.y;
+    const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
+    uint64_t lo[KC][2][FP_COLS] = {}, hi[KC][2][FP_COLS] = {}, top[KC][2][FP_COLS] = {};
+    for (size_t i = r0; i < r1; ++i) {
+        uint64_t x[FP_COLS];
+#pragma unroll
+        for (int q = 0; q < FP_COLS; ++q) x[q] = (j0 + q < cols) ? m[i * cols + j0 + q] : 0;
+#pragma unroll
+        for (int k = 0; k < KC; ++k) {
+            const Fp2 cf = coeffs[(comb0 + k) * rows + i];
+            const uint64_t comp[2] = {cf.c0, cf.c1};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int q = 0; q < FP_COLS; ++q) {
+                    uint64_t pl, ph;
+                    gl::mul_wide(comp[h], x[q], pl, ph);
+                    const uint64_t nl = lo[k][h][q] + pl;
+                    const uint64_t c1 = nl < pl;
+                    const uint64_t t = ph + c1;  // ph <= 2^64-2, no overflow
+                    const uint64_t nh = hi[k][h][q] + t;
+                    top[k][h][q] += (nh < t);
+                    lo[k][h][q] = nl;
+                    hi[k][h][q] = nh;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+        if (comb0 + k >= combinations) break;
+#pragma unroll
+        for (int q = 0; q < FP_COLS; ++q) {
+            const size_t j = j0 + q;
+            if (j >= cols) break;
+            partials[(ck * combinations + comb0 + k) * cols + j] =
+                Fp2{fold192(lo[k][0][q], hi[k][0][q], top[k][0][q]), fold192(lo[k][1][q], hi[k][1][q], top[k][1][q])};
+        }
+    }
+}
+
+__global__ void reduce_partials(const Fp2* partials, Fp2* out, size_t chunks, size_t per_chunk) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < per_chunk; z += stride) {
+        Fp2 acc{0, 0};
+        for (size_t ck = 0; ck < chunks; ++ck) acc = gl::fp2_add(acc, partials[ck * per_chunk + z]);
+        out[z] = acc;
+    }
+}
+
+template <class F>
+static int launch_comb_groups(size_t combinations, F&& f) {
+    for (size_t c0 = 0; c0 < combinations;) {
+        const size_t left = combinations - c0;
+        const int kc = left >= 2 ? 2 : 1;
+        if (f(c0, kc)) return -1;
+        c0 += kc;
+    }
+    return 0;
+}
+
+int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
+                     size_t cols, size_t pad, size_t combinations, Fp2* out) {
+    const size_t msg_len = cols + pad;
+    const size_t chunks = (rows + COMB_CHUNK - 1) / COMB_CHUNK;
+    size_t per_chunk = 0, bytes = 0;
+    if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes))
+        return fail_msg(c, "PCS combination partials overflow size_t");
+    if (chunks > 65535) return fail_msg(c, "PCS combination row count exceeds the supported maximum");
+    if (ensure_ws(c, WS_PARTIALS, bytes)) return -1;
+    Fp2* part = ws<Fp2>(c, WS_PARTIALS);
+    const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
+    const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
+                    static_cast<unsigned>(chunks));
+    // 8-byte row loads need an 8-byte aligned base and a row pitch of 4k i16.
+    const int vec_ok = (reinterpret_cast<uintptr_t>(w) % 8 == 0) && (cols % 4 == 0);
+    if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
+            if (kc == 2)
+                hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs, part,
+                                   rows, cols, msg_len, c0, combinations, COMB_CHUNK, vec_ok);
+            else
+                hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs, part,
+                                   rows, cols, msg_len, c0, combinations, COMB_CHUNK, vec_ok);
+            VMX_HIP(c, hipGetLastError());
+            return 0;
+        }))
+        return -1;
+    if (pad) {
+        const dim3 g(static_cast<unsigned>((pad + 255) / 256), static_cast<unsigned>(chunks),
+                     static_cast<unsigned>(combinations));
+        if (combinations > 65535) return fail_msg(c, "too many PCS combinations");
+        hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs, part, rows, cols, pad,
+                           msg_len, combinations, COMB_CHUNK);
+        VMX_HIP(c, hipGetLastError());
+    }
+    hipLaunchKernelGGL(reduce_partials, dim3(grid_for(per_chunk, 256, 4096)), dim3(256), 0, c->stream,
+                       static_cast<const Fp2*>(part), out, chunks, per_chunk);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, const Fp2* coeffs,
+                    size_t combinations, Fp2* out) {
+    const size_t chunks = (rows + COMB_CHUNK - 1) / COMB_CHUNK;
+    size_t per_chunk = 0, bytes = 0;
+    if (!mul_ok(combinations, cols, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes))
+        return fail_msg(c, "combination partials overflow size_t");
+    if (chunks > 65535) return fail_msg(c, "combination row count exceeds the supported maximum");
+    if (ensure_ws(c, WS_PARTIALS, bytes)) return -1;
+    Fp2* part = ws<Fp2>(c, WS_PARTIALS);
+    const size_t col_threads = (cols + FP_COLS - 1) / FP_COLS;
+    const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
+                    static_cast<unsigned>(chunks));
+    if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
+            if (kc == 2)
+                hipLaunchKernelGGL(combine_fp_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, m, coeffs, part,
+                                   rows, cols, c0, combinations, COMB_CHUNK);
+            else
+                hipLaunchKernelGGL(combine_fp_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, m, coeffs, part,
+                                   rows, cols, c0, combinations, COMB_CHUNK);
+            VMX_HIP(c, hipGetLastError());
+            return 0;
+        }))
+        return -1;
+    hipLaunchKernelGGL(reduce_partials, dim3(grid_for(per_chunk, 256, 4096)), dim3(256), 0, c->stream,
+                       static_cast<const Fp2*>(part), out, chunks, per_chunk);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// ---- Fp2 powers [c^1..c^count] (reference fp2_powers_kernel runs serially) ---------------
+
+__global__ void fp2_powers_kernel(Fp2 base, Fp2* out, size_t count) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        // c^(i+1) by square-and-multiply; each element independent.
+        uint64_t e = i + 1;
+        Fp2 acc{1, 0}, b = base;
+        while (e) {
+            if (e & 1) acc = gl::fp2_mul(acc, b);
+            b = gl::fp2_mul(b, b);
+            e >>= 1;
+        }
+        out[i] = acc;
+    }
+}
+
+int fp2_powers(Context* c, Fp2 base, Fp2* out, size_t count) {
+    hipLaunchKernelGGL(fp2_powers_kernel, dim3(grid_for(count, 256, 8192)), dim3(256), 0, c->stream, base, out,
+                       count);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+__global__ void fp2_add_kernel(Fp2* t, const Fp2* a, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        t[i] = gl::fp2_add(t[i], a[i]);
+}
+
+int fp2_add_inplace(Context* c, Fp2* target, const Fp2* add, size_t n) {
+    hipLaunchKernelGGL(fp2_add_kernel, dim3(grid_for(n, 256, 1 << 16)), dim3(256), 0, c->stream, target, add, n);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// ---- column gathers (reference .cu:3008-3024) ------------------------------------------------
+
+template <typename T>
+__global__ void gather_kernel(const T* m, const uint32_t* idx, T* out, size_t rows, size_t cols, size_t queries) {
+    const size_t total = rows * queries;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < total; z += stride) {
+        const size_t q = z / rows, i = z - q * rows;
+        const uint32_t col = idx[q];
+        // Out-of-range indices read as zero instead of faulting; the Rust seam
+        // validates indices before upload (rust/volta-accel/src/lib.rs:6773-6827).
+        out[z] = col < cols ? m[i * cols + col] : T{};
+    }
+}
+
+int gather_columns(Context* c, const uint64_t* m, const uint32_t* idx, uint64_t* out, size_t rows, size_t cols,
+                   size_t queries, bool fp2) {
+    const unsigned g = grid_for(rows * queries, 256, 1 << 16);
+    if (fp2)
+        hipLaunchKernelGGL(gather_kernel<Fp2>, dim3(g), dim3(256), 0, c->stream, reinterpret_cast<const Fp2*>(m), idx,
+                           reinterpret_cast<Fp2*>(out), rows, cols, queries);
+    else
+        hipLaunchKernelGGL(gather_kernel<uint64_t>, dim3(g), dim3(256), 0, c->stream, m, idx, out, rows, cols,
+                           queries);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// ---- ChaCha8 FpStream rows (reference .cu:1345-1372; one stream per row) ---------------------
+
+__global__ void chacha8_rows_kernel(chacha8::Key key, uint64_t base_domain, size_t rows, size_t count,
+                                    uint64_t* out) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t r = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < rows; r += stride) {
+        chacha8::FpStream s(key, base_domain + r);
+        uint64_t* o = out + r * count;
+        for (size_t j = 0; j < count; ++j) o[j] = s.next_fp();
+    }
+}
+
+__global__ void chacha8_fp2_rows_kernel(chacha8::Key key, uint64_t base_domain, size_t rows, size_t count,
+                                        size_t padded, Fp2* out) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t r = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < rows; r += stride) {
+        chacha8::FpStream s(key, base_domain + r);
+        Fp2* o = out + r * padded;
+        for (size_t j = 0; j < count; ++j) {
+            const uint64_t a = s.next_fp();
+            const uint64_t b = s.next_fp();
+            o[j] = Fp2{a, b};
+        }
+        for (size_t j = count; j < padded; ++j) o[j] = Fp2{0, 0};
+    }
+}
+
+int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
+                    uint64_t* out) {
+    const chacha8::Key key = chacha8::key_from_seed(seed);
+    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, 64, 65535)), dim3(64), 0, c->stream, key,
+                       base_domain, rows, count, out);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
+                            size_t padded, Fp2* out) {
+    const chacha8::Key key = chacha8::key_from_seed(seed);
+    hipLaunchKernelGGL(chacha8_fp2_rows_kernel, dim3(grid_for(rows, 64, 65535)), dim3(64), 0, c->stream, key,
+                       base_domain, rows, count, padded, out);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// ---- measurement probes ---------------------------------------------------------------------------
+
+// Streaming copy with 16-byte accesses: the achievable-bandwidth yardstick.
+__global__ __launch_bounds__(256) void copy_kernel(const uint4* src, uint4* dst, size_t n16) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+        dst[i] = src[i];
+}
+
+int probe_copy(Context* c, const void* src, void* dst, size_t bytes) {
+    const size_t n16 = bytes / 16;
+    hipLaunchKernelGGL(copy_kernel, dim3(grid_for(n16, 256 * 8, 256 * 64)), dim3(256), 0, c->stream,
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+// The reference's Fp2 roofline probes (cuda/p7_goldilocks_roofline.cu:74-89).
+__global__ void fp2_stream_kernel(const Fp2* a, const Fp2* b, Fp2* out, size_t n) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = gl::fp2_mul(a[i], b[i]);
+}
+
+__global__ void fp2_chain_kernel(const Fp2* a, const Fp2* b, Fp2* out, size_t n, int rounds) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) {
+        Fp2 x = a[i];
+        const Fp2 y = b[i];
+        for (int j = 0; j < rounds; ++j)
+            x = gl::fp2_add(gl::fp2_mul(x, y), Fp2{static_cast<uint64_t>(j + 1), static_cast<uint64_t>(2 * j + 3)});
+        out[i] = x;
+    }
+}
+
+int probe_fp2_stream(Context* c, const Fp2* a, const Fp2* b, Fp2* out, size_t n) {
+    hipLaunchKernelGGL(fp2_stream_kernel, dim3(grid_for(n, 256, 1 << 16)), dim3(256), 0, c->stream, a, b, out, n);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+int probe_fp2_chain(Context* c, const Fp2* a, const Fp2* b, Fp2* out, size_t n, int rounds) {
+    hipLaunchKernelGGL(fp2_chain_kernel, dim3(grid_for(n, 256, 1 << 16)), dim3(256), 0, c->stream, a, b, out, n,
+                       rounds);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+}  // namespace vmx
