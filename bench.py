@@ -1,0 +1,298 @@
+#!/usr/bin/env python3
+"""Benchmark of the Ligero RS-encode hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3]
+
+One step = one pass of the hot path over the resident synthetic batch of the
+chosen configuration (default C3, the full GPT-2-small weight commit):
+RS-encode of every row (fused i16 lift + NTT) plus the two challenge-power
+row combinations (Fp2 powers + one combination pass).  Inputs are resident
+in HBM before timing starts; outputs stay resident.
+
+Prints one JSON line: whole-step throughput in codeword Gelem/s, the
+roofline of the dominant kernel (the encode) from HIP events recorded by the
+library on its own stream, and a CPU baseline (the oracle restatement of the
+reference CPU path, OpenMP over the host cores) on the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "volta-zk_amd"))
+
+METRIC = "Ligero RS-encode Gelem/s (Goldilocks NTT) + % HBM roofline, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+WORKLOADS = {
+    "c1": "c1: 256 x 2^12 uniform Fp (FpStream rows) -> 2^14 (rate 1/4) + 1 combination of 256 rows",
+    "c2": "c2: GPT-2 c_attn 768x2304 i16 packed 1024 x 2^11 -> 2^13 (rate 1/4) + 2 challenge-power combinations",
+    "c3": "c3: full GPT-2-small weights 124,439,808 i16 packed 2^16 x 2^11 -> 2^13 (rate 1/4) "
+          "+ 2 challenge-power combinations",
+    "c4": "c4: 2^15 x 2^12 packed-lane Fp -> 2^15 (rate 1/8)",
+    "c5": "c5: 64 x 2^24 uniform Fp, forward + inverse NTT + 64-row combination + 256-column gather",
+}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Resident inputs/outputs and one step as raw C-ABI calls (no allocation
+    inside a step)."""
+
+    def __init__(self, b, name: str):
+        import numpy as np
+
+        from volta_mi355x import FP2
+        from volta_mi355x import workloads as W
+        self.b, self.lib, self.raw, self.name = b, b.lib, b.raw, name
+        cfg = self.cfg = W.CONFIGS[name]
+        self.np = np
+        rows, n = cfg.rows, cfg.n
+        self.bufs = []
+
+        def keep(x):
+            self.bufs.append(x)
+            return x
+
+        if name in ("c2", "c3"):
+            w = W.c3_weights() if name == "c3" else W.c2_weights()
+            self.host_w = w
+            self.w = keep(b.upload_device(w.reshape(-1)))
+            self.pads = keep(b.alloc_device(1, np.uint64))
+            self.enc = keep(b.alloc_device(rows * n, np.uint64))
+            self.challenges = W.challenges_fp2(f"volta-mi355x/{name}/challenges", cfg.combinations)
+            self.coeffs = keep(b.alloc_device(cfg.combinations * rows, FP2))
+            self.u = keep(b.alloc_device(cfg.combinations * cfg.msg_len, FP2))
+        elif name == "c1":
+            self.msgs = keep(b.chacha8_prover_secret_fp_rows_device(W.SEED_C1_ROWS, 0, rows, cfg.msg_len))
+            self.enc = keep(b.alloc_device(rows * n, np.uint64))
+            ch = W.uniform_fp("volta-mi355x/c1/challenges", rows)
+            co = np.zeros((rows, 2), np.uint64)
+            co[:, 0] = ch
+            self.coeffs = keep(b.alloc_device(rows, FP2))
+            b.upload_into(self.coeffs, 0, co.reshape(-1))
+            self.u = keep(b.alloc_device(cfg.msg_len, FP2))
+        elif name == "c4":
+            m = W.c4_messages()
+            self.msgs = keep(b.upload_device(m.reshape(-1)))
+            del m
+            self.enc = keep(b.alloc_device(rows * n, np.uint64))
+        elif name == "c5":
+            x = W.c5_rows()
+            self.msgs = keep(b.upload_device(x.reshape(-1)))
+            del x
+            self.enc = keep(b.alloc_device(rows * n, np.uint64))
+            self.back = keep(b.alloc_device(rows * n, np.uint64))
+            self.challenges = W.challenges_fp2("volta-mi355x/c5/challenges", 1)
+            self.coeffs = keep(b.alloc_device(rows, FP2))
+            self.u = keep(b.alloc_device(n, FP2))
+            q = W.c5_query_columns(n, 256)
+            self.idx = keep(b.upload_device(q))
+            self.cols_out = keep(b.alloc_device(rows * 256, np.uint64))
+        else:
+            raise SystemExit(f"unknown config {name}")
+
+    def _ok(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.b.last_error())
+
+    def step(self):
+        L, r, cfg = self.lib, self.raw, self.cfg
+        rows, n = cfg.rows, cfg.n
+        if self.name in ("c2", "c3"):
+            self._ok(L.volta_mi355x_pcs_encode_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, 0, n,
+                                                      self.enc.id, 0))
+            for k, c in enumerate(self.challenges):
+                self._ok(L.volta_cuda_fp2_powers_device(r, int(c[0]), int(c[1]), self.coeffs.id, k * rows, rows))
+            self._ok(L.volta_cuda_pcs_combine_rows_device(r, self.w.id, 0, self.pads.id, 0, self.coeffs.id, 0, rows,
+                                                          cfg.msg_len, 0, cfg.combinations, self.u.id, 0))
+        elif self.name == "c1":
+            self._ok(L.volta_mi355x_ntt_fp_encode_device(r, self.msgs.id, 0, rows, cfg.msg_len, n, self.enc.id, 0))
+            self._ok(L.volta_mi355x_combine_rows_fp_device(r, self.msgs.id, 0, rows, cfg.msg_len, self.coeffs.id, 0,
+                                                           1, self.u.id, 0))
+        elif self.name == "c4":
+            self._ok(L.volta_mi355x_ntt_fp_encode_device(r, self.msgs.id, 0, rows, cfg.msg_len, n, self.enc.id, 0))
+        elif self.name == "c5":
+            self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
+            self._ok(L.volta_mi355x_ntt_fp_inverse_batch_device(r, self.enc.id, 0, rows, n, self.back.id, 0))
+            c = self.challenges[0]
+            self._ok(L.volta_cuda_fp2_powers_device(r, int(c[0]), int(c[1]), self.coeffs.id, 0, rows))
+            self._ok(L.volta_mi355x_combine_rows_fp_device(r, self.enc.id, 0, rows, n, self.coeffs.id, 0, 1,
+                                                           self.u.id, 0))
+            self._ok(L.volta_cuda_pcs_gather_columns_device(r, self.enc.id, 0, rows, n, self.idx.id, 0, 256,
+                                                            self.cols_out.id, 0, 0))
+
+    def elements_per_step(self) -> int:
+        # codeword elements produced (C5 counts forward and inverse outputs)
+        return self.cfg.elements * (2 if self.name == "c5" else 1)
+
+    def close(self):
+        for x in self.bufs:
+            self.b.free_device(x)
+
+
+def copy_bandwidth(b, nbytes: int = 1 << 32, reps: int = 10) -> float:
+    """Achievable HBM bandwidth from a 16-byte streaming copy (read+write)."""
+    import numpy as np
+    src = b.alloc_device(nbytes // 8, np.uint64)
+    dst = b.alloc_device(nbytes // 8, np.uint64)
+    b.zero_device(src, 0, nbytes // 8)
+    L, r = b.lib, b.raw
+    L.volta_mi355x_probe_copy_device(r, src.id, dst.id, nbytes)
+    b.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        if L.volta_mi355x_probe_copy_device(r, src.id, dst.id, nbytes) != 0:
+            raise RuntimeError(b.last_error())
+    b.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    b.free_device(src)
+    b.free_device(dst)
+    return 2 * nbytes / dt / 1e9
+
+
+def cpu_baseline(name: str, wl: Workload) -> dict:
+    """The oracle's restatement of the reference CPU path (per-row radix-2 DIT
+    NttPlan::forward + combine_rows), OpenMP over this host's cores."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+    oracle.build()
+    from volta_mi355x import workloads as W
+    cfg = W.CONFIGS[name]
+    threads = oracle.default_threads()
+    if name not in ("c2", "c3"):
+        return None
+    w = wl.host_w
+    co = np.concatenate([oracle.fp2_powers(tuple(int(x) for x in c), cfg.rows) for c in wl.challenges])
+
+    def run(rows):
+        oracle.pcs_encode_i16(w[:rows].reshape(-1), None, rows, cfg.msg_len, 0, cfg.n, threads)
+        cr = np.concatenate([co[k * cfg.rows:k * cfg.rows + rows] for k in range(cfg.combinations)])
+        oracle.pcs_combine_rows(w[:rows].reshape(-1), None, cr, rows, cfg.msg_len, 0, cfg.combinations, threads)
+
+    t0 = time.perf_counter()
+    run(min(cfg.rows, 1024))
+    per_row = (time.perf_counter() - t0) / min(cfg.rows, 1024)
+    # bounded sample: at most ~20 s of wall time over 3 timed runs
+    sample = int(min(cfg.rows, max(1024, 6.0 / max(per_row, 1e-9))))
+    sample -= sample % 1024 or 0
+    sample = max(sample, min(cfg.rows, 1024))
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run(sample)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {
+        "value": round(sample * cfg.n / t / 1e9, 4),
+        "unit": "Gelem/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{sample} of {cfg.rows} rows of {name} (encode + {cfg.combinations} combinations over those rows), "
+                  f"median of 3 after 1 warmup, {t:.3f} s",
+    }
+
+
+def traffic_for(name: str):
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(name)
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-copy-probe", action="store_true")
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: every box in this setup has one MI355X and the encode path is "
+              "row-parallel with no exchange; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    from volta_mi355x import Backend
+    b = Backend(timing_policy=0)
+    log(f"config {a.config}: generating and uploading inputs")
+    wl = Workload(b, a.config)
+    cfg = wl.cfg
+    for _ in range(a.warmup):
+        wl.step()
+    b.synchronize()
+    b.reset_stats()
+    log(f"timing {a.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        wl.step()
+    b.synchronize()
+    dt = time.perf_counter() - t0
+    stats = b.get_stats()
+    ms = dt / a.steps * 1e3
+    value = wl.elements_per_step() * a.steps / dt / 1e9
+    enc_calls = stats["calls"]["pcs_ntt"]
+    enc_s = stats["kernel_ns"]["pcs_ntt"] / max(enc_calls, 1) / 1e9
+    launches_per_step = max(enc_calls // a.steps, 1)
+    alg = cfg.algorithmic_bytes  # per encode launch (C5: one direction)
+    achieved = alg / enc_s / 1e9 if enc_s > 0 else None
+    copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
+    wl_close = wl.close
+    cpu = None
+    if not a.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(a.config, wl)
+    wl_close()
+    b.close()
+    out = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "Gelem/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {"workload": WORKLOADS[a.config], "rows": cfg.rows, "msg_len": cfg.msg_len, "code_len": cfg.n,
+                   "combinations": cfg.combinations, "parallelism": "single-gpu"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "encode (PcsNtt launch)",
+            "achieved": round(achieved, 1) if achieved else None,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
+            "traffic": traffic_for(a.config),
+            "algorithmic_bytes": alg,
+            "avg_launch_ms": round(enc_s * 1e3, 4),
+            "launches_per_step": launches_per_step,
+            "hbm_copy_gbs": copy_gbs,
+        },
+        "cpu_baseline": cpu,
+        "kernel_ms_per_step": {k: round(v / a.steps / 1e6, 4) for k, v in stats["kernel_ns"].items() if v},
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,256 @@
+"""GPU parity of the transforms, through the C ABI, against the oracle and the
+reference-recorded checksums.  Bit-exact everywhere (integer field work)."""
+import random
+
+import numpy as np
+import pytest
+
+import spike_inputs as spike
+
+pytestmark = pytest.mark.gpu
+
+P = spike.P
+
+
+def rand_fp(seed, shape):
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, P, size=shape, dtype=np.uint64)
+
+
+def run_ntt(backend, host, n):
+    rows = host.size // n
+    inp = backend.upload_device(host.reshape(-1))
+    try:
+        out = backend.ntt_fp_batch_device(inp, rows, n)
+        try:
+            return backend.download_device(out).reshape(rows, n)
+        finally:
+            backend.free_device(out)
+    finally:
+        backend.free_device(inp)
+
+
+# ---- field arithmetic on the device, pinned by reference-recorded outputs ------
+
+def test_fp2_stream_probe_matches_reference_checksum(backend, oracle):
+    log2, expected = spike.FP2_STREAM_GOLDEN[0]
+    a, b = spike.fp2_inputs(1 << log2)
+    da, db = backend.upload_device(a.reshape(-1)), backend.upload_device(b.reshape(-1))
+    out = backend.alloc_device(2 << log2, np.uint64)
+    backend._check(backend.lib.volta_mi355x_probe_fp2_device(backend.raw, da.id, db.id, out.id, 1 << log2, 0))
+    got = backend.download_device(out)
+    for buf in (da, db, out):
+        backend.free_device(buf)
+    assert oracle.fnv(got) == expected
+
+
+def test_fp2_chain_probe_matches_reference_checksum(backend, oracle):
+    log2, rounds, expected = spike.FP2_CHAIN_GOLDEN[0]
+    a, b = spike.fp2_inputs(1 << log2)
+    da, db = backend.upload_device(a.reshape(-1)), backend.upload_device(b.reshape(-1))
+    out = backend.alloc_device(2 << log2, np.uint64)
+    backend._check(backend.lib.volta_mi355x_probe_fp2_device(backend.raw, da.id, db.id, out.id, 1 << log2, rounds))
+    got = backend.download_device(out)
+    for buf in (da, db, out):
+        backend.free_device(buf)
+    assert oracle.fnv(got) == expected
+
+
+# ---- forward NTT -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", list(range(1, 15)))
+def test_ntt_lds_sizes_match_oracle(backend, oracle, bits):
+    n = 1 << bits
+    host = rand_fp(bits, (3, n))
+    host[0, :min(4, n)] = [0, 1, P - 1, P - 2][:min(4, n)]  # boundary values
+    assert (run_ntt(backend, host, n) == oracle.ntt_forward_batch(host)).all()
+
+
+@pytest.mark.parametrize("bits,rows", [(15, 3), (16, 2), (17, 2), (19, 1)])
+def test_ntt_four_step_sizes_match_oracle(backend, oracle, bits, rows):
+    n = 1 << bits
+    host = rand_fp(100 + bits, (rows, n))
+    assert (run_ntt(backend, host, n) == oracle.ntt_forward_batch(host)).all()
+
+
+@pytest.mark.parametrize("rows,bits,msg_len,expected", spike.NTT_GOLDEN)
+def test_ntt_reference_checksums_on_device(backend, oracle, rows, bits, msg_len, expected):
+    out = run_ntt(backend, spike.ntt_input(rows, bits, msg_len), 1 << bits)
+    assert oracle.fnv(out) == expected
+
+
+def test_ntt_offsets_and_input_preserved(backend, oracle):
+    n, rows = 256, 4
+    host = rand_fp(7, (rows, n))
+    big = backend.alloc_device(rows * n + 3 * n, np.uint64)
+    backend.upload_into(big, n, host.reshape(-1))
+    out = backend.alloc_device(rows * n + 5, np.uint64)
+    backend._check(backend.lib.volta_cuda_ntt_fp_batch_device(backend.raw, big.id, n, rows, n, out.id, 5))
+    got = backend.download_device(out, 5, rows * n).reshape(rows, n)
+    still = backend.download_device(big, n, rows * n).reshape(rows, n)
+    backend.free_device(big)
+    backend.free_device(out)
+    assert (got == oracle.ntt_forward_batch(host)).all()
+    assert (still == host).all()
+
+
+def test_inverse_round_trip_and_oracle(backend, oracle):
+    for bits, rows in [(6, 3), (13, 4), (16, 2)]:
+        n = 1 << bits
+        host = rand_fp(200 + bits, (rows, n))
+        inp = backend.upload_device(host.reshape(-1))
+        fwd = backend.ntt_fp_batch_device(inp, rows, n)
+        inv = backend.ntt_fp_inverse_batch_device(fwd, rows, n)
+        back = backend.download_device(inv).reshape(rows, n)
+        inv_of_host = backend.ntt_fp_inverse_batch_device(inp, rows, n)
+        direct = backend.download_device(inv_of_host).reshape(rows, n)
+        for b in (inp, fwd, inv, inv_of_host):
+            backend.free_device(b)
+        assert (back == host).all()
+        assert (direct == oracle.ntt_inverse_batch(host)).all()
+
+
+def test_host_entry_points(backend, oracle):
+    n = 1 << 10
+    msgs = rand_fp(11, (5, 300))
+    got = backend.ntt_fp_batch(msgs, 5, 300, n)
+    assert (got == oracle.ntt_encode_batch(msgs, n)).all()
+    one = backend.ntt_fp(msgs[0], n)
+    assert (one == got[0]).all()
+    f2 = rand_fp(12, (40, 2))
+    got2 = backend.ntt_fp2(f2, 64)
+    for comp in (0, 1):
+        want = oracle.ntt_encode_batch(f2[:, comp].reshape(1, -1).copy(), 64)[0]
+        assert (got2[:, comp] == want).all()
+
+
+def test_fp2_batch_device_componentwise(backend, oracle):
+    rows, n = 3, 1 << 12
+    host = rand_fp(13, (rows, n, 2))
+    from volta_mi355x import FP2
+    inp2 = backend.alloc_device(rows * n, FP2)
+    backend.upload_into(inp2, 0, host.reshape(-1))
+    out = backend.ntt_fp2_batch_device(inp2, rows, n)
+    got = backend.download_device(out).view(np.uint64).reshape(rows, n, 2)
+    for b in (inp2, out):
+        backend.free_device(b)
+    for comp in (0, 1):
+        assert (got[:, :, comp] == oracle.ntt_forward_batch(host[:, :, comp].copy())).all()
+
+
+def test_compact_encode_device(backend, oracle):
+    for rows, msg_len, bits in [(7, 100, 9), (4, 4096, 14), (3, 1000, 16)]:
+        n = 1 << bits
+        msgs = rand_fp(300 + bits, (rows, msg_len))
+        d = backend.upload_device(msgs.reshape(-1))
+        out = backend.ntt_fp_encode_device(d, rows, msg_len, n)
+        got = backend.download_device(out).reshape(rows, n)
+        backend.free_device(d)
+        backend.free_device(out)
+        assert (got == oracle.ntt_encode_batch(msgs, n)).all()
+
+
+# ---- PCS encode of i16 message rows ---------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols,pad,bits", [(5, 16, 0, 6), (9, 100, 7, 8), (17, 2048, 0, 13), (4, 2048, 512, 13),
+                                                (3, 4096, 0, 14), (2, 1024, 3, 15)])
+def test_pcs_encode_fused_and_chain_match_oracle(backend, oracle, rows, cols, pad, bits):
+    n = 1 << bits
+    g = np.random.Generator(np.random.PCG64(rows * 1000 + cols))
+    w = g.integers(-(1 << 15), 1 << 15, size=rows * cols, dtype=np.int16)
+    w[:3] = [-32768, 32767, -1]
+    pads = rand_fp(cols, rows * pad) if pad else np.zeros(1, np.uint64)
+    dw, dp = backend.upload_device(w), backend.upload_device(pads)
+    fused = backend.pcs_encode_device(dw, 0, dp, 0, rows, cols, pad, n)
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, pad, n)
+    chain = backend.ntt_fp_batch_device(msgs, rows, n)
+    got_f = backend.download_device(fused).reshape(rows, n)
+    got_m = backend.download_device(msgs).reshape(rows, n)
+    got_c = backend.download_device(chain).reshape(rows, n)
+    for b in (dw, dp, fused, msgs, chain):
+        backend.free_device(b)
+    want = oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)
+    assert (got_m == oracle.pcs_messages(w, pads, rows, cols, pad, n)).all()
+    assert (got_c == want).all()
+    assert (got_f == want).all()
+
+
+# ---- benchmark configurations ---------------------------------------------------------
+
+def test_c1_full_config(backend, oracle):
+    """C1: 256 rows of FpStream-generated messages -> 2^14 codewords."""
+    from volta_mi355x import workloads as W
+    cfg = W.CONFIGS["c1"]
+    dm = backend.chacha8_prover_secret_fp_rows_device(W.SEED_C1_ROWS, 0, cfg.rows, cfg.msg_len)
+    msgs = backend.download_device(dm).reshape(cfg.rows, cfg.msg_len)
+    assert (msgs == oracle.fp_rows(W.SEED_C1_ROWS, 0, cfg.rows, cfg.msg_len)).all()
+    out = backend.ntt_fp_encode_device(dm, cfg.rows, cfg.msg_len, cfg.n)
+    got = backend.download_device(out).reshape(cfg.rows, cfg.n)
+    backend.free_device(dm)
+    backend.free_device(out)
+    assert (got == oracle.ntt_encode_batch(msgs, cfg.n)).all()
+
+
+def test_c2_full_config(backend, oracle):
+    from volta_mi355x import workloads as W
+    cfg = W.CONFIGS["c2"]
+    w = W.c2_weights()
+    dw, dp = backend.upload_device(w.reshape(-1)), backend.alloc_device(1, np.uint64)
+    out = backend.pcs_encode_device(dw, 0, dp, 0, cfg.rows, cfg.msg_len, 0, cfg.n)
+    got = backend.download_device(out).reshape(cfg.rows, cfg.n)
+    for b in (dw, dp, out):
+        backend.free_device(b)
+    assert (got == oracle.pcs_encode_i16(w, None, cfg.rows, cfg.msg_len, 0, cfg.n)).all()
+
+
+def test_c3_full_config_sampled_rows(backend, oracle):
+    """C3 at full size (2^16 rows); every 61st row and the last rows are checked
+    against the oracle, and the whole output by a linear invariant: the sum of
+    all codewords equals the encode of the sum of all messages."""
+    from volta_mi355x import workloads as W
+    cfg = W.CONFIGS["c3"]
+    w = W.c3_weights()
+    dw, dp = backend.upload_device(w.reshape(-1)), backend.alloc_device(1, np.uint64)
+    out = backend.pcs_encode_device(dw, 0, dp, 0, cfg.rows, cfg.msg_len, 0, cfg.n)
+    rows = list(range(0, cfg.rows, 61)) + list(range(cfg.rows - 4, cfg.rows))
+    got = np.stack([backend.download_device(out, r * cfg.n, cfg.n) for r in rows])
+    want = oracle.pcs_encode_i16(w[rows].reshape(-1), None, len(rows), cfg.msg_len, 0, cfg.n)
+    assert (got == want).all()
+    # column sums via the combination with all-one coefficients (u64 rows)
+    ones = backend.upload_device(np.tile(np.array([1, 0], np.uint64), cfg.rows))
+    colsum = backend.combine_rows_fp_device(out, cfg.rows, cfg.n, ones, 1)
+    s = backend.download_device(colsum).view(np.uint64).reshape(cfg.n, 2)
+    for b in (dw, dp, out, ones, colsum):
+        backend.free_device(b)
+    msum = w.astype(np.int64).sum(axis=0)
+    msum = np.where(msum < 0, msum.astype(np.uint64) + np.uint64(P), msum.astype(np.uint64))
+    want_sum = oracle.ntt_encode_batch(msum.astype(np.uint64).reshape(1, -1), cfg.n)[0]
+    assert (s[:, 1] == 0).all()
+    assert (s[:, 0] == want_sum).all()
+
+
+def test_c4_rows(backend, oracle):
+    from volta_mi355x import workloads as W
+    cfg = W.CONFIGS["c4"]
+    rows = 24
+    m = W.c4_messages(rows, cfg.msg_len)
+    d = backend.upload_device(m.reshape(-1))
+    out = backend.ntt_fp_encode_device(d, rows, cfg.msg_len, cfg.n)
+    got = backend.download_device(out).reshape(rows, cfg.n)
+    backend.free_device(d)
+    backend.free_device(out)
+    assert (got == oracle.ntt_encode_batch(m, cfg.n)).all()
+
+
+def test_c5_rows_forward_inverse(backend, oracle):
+    """Two 2^24 rows: forward vs oracle, then the inverse restores the input."""
+    rows, n = 2, 1 << 24
+    host = rand_fp(55, (rows, n))
+    inp = backend.upload_device(host.reshape(-1))
+    fwd = backend.ntt_fp_batch_device(inp, rows, n)
+    got = backend.download_device(fwd).reshape(rows, n)
+    inv = backend.ntt_fp_inverse_batch_device(fwd, rows, n)
+    back = backend.download_device(inv).reshape(rows, n)
+    for b in (inp, fwd, inv):
+        backend.free_device(b)
+    assert (back == host).all()
+    assert (got == oracle.ntt_forward_batch(host)).all()

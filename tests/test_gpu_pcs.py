@@ -1,0 +1,297 @@
+"""GPU parity of the PCS row primitives through the C ABI: combinations,
+messages, powers, adds, gathers, ChaCha8 rows; plus the seam's error and
+stats contract (rust/volta-pcs/tests/cuda.rs:186-547 and
+rust/volta-accel/src/lib.rs:7587-8435 are the reference's own checks)."""
+import numpy as np
+import pytest
+
+import spike_inputs as spike
+
+pytestmark = pytest.mark.gpu
+
+P = spike.P
+
+
+def rand_fp(seed, shape):
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, P, size=shape, dtype=np.uint64)
+
+
+def rand_i16(seed, size):
+    return np.random.Generator(np.random.PCG64(seed)).integers(-(1 << 15), 1 << 15, size=size, dtype=np.int16)
+
+
+# ---- combinations ------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols,pad,comb,w_off", [
+    (1, 1, 0, 1, 0), (7, 11, 3, 4, 0), (300, 2048, 0, 2, 0), (129, 13, 5, 3, 1), (1000, 64, 512, 1, 3),
+    (4097, 8, 0, 2, 0),
+])
+def test_combine_rows_device_matches_oracle(backend, oracle, rows, cols, pad, comb, w_off):
+    w = rand_i16(rows + cols, rows * cols)
+    w[:2] = [-32768, 32767][:w.size]
+    pads = rand_fp(rows * 7 + pad, rows * pad) if pad else np.zeros(1, np.uint64)
+    co = rand_fp(comb + 99, (comb * rows, 2))
+    # a leading offset exercises unaligned weight rows
+    dw = backend.alloc_device(w_off + w.size, np.int16)
+    backend.upload_into(dw, w_off, w)
+    dp, dc = backend.upload_device(pads), backend.upload_device(co.reshape(-1))
+    from volta_mi355x import FP2
+    dc2 = backend.alloc_device(comb * rows, FP2)
+    backend.upload_into(dc2, 0, co.reshape(-1))
+    out = backend.pcs_combine_rows_device(dw, w_off, dp, 0, dc2, 0, rows, cols, pad, comb)
+    got = backend.download_device(out).view(np.uint64).reshape(comb, cols + pad, 2)
+    for b in (dw, dp, dc, dc2, out):
+        backend.free_device(b)
+    assert (got == oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)).all()
+
+
+def test_combine_rows_host_entry_point(backend, oracle):
+    rows, cols, pad, comb = 33, 40, 6, 2
+    w = rand_i16(1, rows * cols)
+    pads = rand_fp(2, rows * pad)
+    co = rand_fp(3, (comb * rows, 2))
+    got = backend.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)
+    assert (got == oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)).all()
+
+
+@pytest.mark.parametrize("rows,cols,expected", spike.COMBINE_GOLDEN)
+def test_combine_fp_rows_reference_checksums_on_device(backend, oracle, rows, cols, expected):
+    w, q, c = spike.combine_inputs(rows, cols)
+    dm = backend.upload_device(w.reshape(-1))
+    from volta_mi355x import FP2
+    dc = backend.alloc_device(2 * rows, FP2)
+    backend.upload_into(dc, 0, np.concatenate([q, c]).reshape(-1))
+    out = backend.combine_rows_fp_device(dm, rows, cols, dc, 2)
+    u = backend.download_device(out).view(np.uint64).reshape(2, cols, 2)
+    for b in (dm, dc, out):
+        backend.free_device(b)
+    assert spike.combine_checksum(oracle.fnv, u[0], u[1]) == expected
+
+
+def test_combine_fp_rows_matches_oracle_odd_shape(backend, oracle):
+    rows, cols, comb = 257, 37, 3
+    m = rand_fp(5, (rows, cols))
+    m[0, :3] = [P - 1, P - 1, 0]
+    co = rand_fp(6, (comb * rows, 2))
+    co[:2] = P - 1
+    dm = backend.upload_device(m.reshape(-1))
+    from volta_mi355x import FP2
+    dc = backend.alloc_device(comb * rows, FP2)
+    backend.upload_into(dc, 0, co.reshape(-1))
+    out = backend.combine_rows_fp_device(dm, rows, cols, dc, comb)
+    got = backend.download_device(out).view(np.uint64).reshape(comb, cols, 2)
+    for b in (dm, dc, out):
+        backend.free_device(b)
+    assert (got == oracle.combine_rows_fp(m, co, comb)).all()
+
+
+def test_proximity_combinations_c2(backend, oracle):
+    """C2's two challenge-power combinations (coefficients c^1..c^rows)."""
+    from volta_mi355x import ligero, workloads as W
+    cfg = W.CONFIGS["c2"]
+    w = W.c2_weights()
+    chs = W.challenges_fp2("volta-mi355x/c2/challenges", 2)
+    params = ligero.LigeroParams(cfg.rows, 11, 0, 13)
+    dw = backend.upload_device(w.reshape(-1))
+    out = ligero.proximity_combinations(backend, dw, None, params, chs)
+    got = backend.download_device(out).view(np.uint64).reshape(2, cfg.msg_len, 2)
+    backend.free_device(dw)
+    backend.free_device(out)
+    co = np.concatenate([oracle.fp2_powers(tuple(int(x) for x in c), cfg.rows) for c in chs])
+    assert (got == oracle.pcs_combine_rows(w, None, co, cfg.rows, cfg.msg_len, 0, 2)).all()
+
+
+def test_proximity_combinations_c3_full(backend, oracle):
+    from volta_mi355x import ligero, workloads as W
+    cfg = W.CONFIGS["c3"]
+    w = W.c3_weights()
+    chs = W.challenges_fp2("volta-mi355x/c3/challenges", 2)
+    params = ligero.LigeroParams(cfg.rows, 11, 0, 13)
+    dw = backend.upload_device(w.reshape(-1))
+    out = ligero.proximity_combinations(backend, dw, None, params, chs)
+    got = backend.download_device(out).view(np.uint64).reshape(2, cfg.msg_len, 2)
+    backend.free_device(dw)
+    backend.free_device(out)
+    co = np.concatenate([oracle.fp2_powers(tuple(int(x) for x in c), cfg.rows) for c in chs])
+    assert (got == oracle.pcs_combine_rows(w, None, co, cfg.rows, cfg.msg_len, 0, 2)).all()
+
+
+def test_linearity_ties_combination_to_encode(backend, oracle):
+    """The verifier's identity (rust/volta-pcs/src/ligero.rs:1841-1856):
+    encode(sum_i r_i m_i) = sum_i r_i encode(m_i)."""
+    rows, cols, n = 64, 512, 2048
+    w = rand_i16(21, rows * cols)
+    co = rand_fp(22, (rows, 2))
+    dw, dp = backend.upload_device(w), backend.alloc_device(1, np.uint64)
+    from volta_mi355x import FP2
+    dc = backend.alloc_device(rows, FP2)
+    backend.upload_into(dc, 0, co.reshape(-1))
+    enc = backend.pcs_encode_device(dw, 0, dp, 0, rows, cols, 0, n)
+    lhs_msg = backend.pcs_combine_rows_device(dw, 0, dp, 0, dc, 0, rows, cols, 0, 1)
+    rhs = backend.combine_rows_fp_device(enc, rows, n, dc, 1)
+    u = backend.download_device(lhs_msg).view(np.uint64).reshape(cols, 2)
+    r = backend.download_device(rhs).view(np.uint64).reshape(n, 2)
+    for b in (dw, dp, dc, enc, lhs_msg, rhs):
+        backend.free_device(b)
+    for comp in (0, 1):
+        want = oracle.ntt_encode_batch(u[:, comp].reshape(1, -1).copy(), n)[0]
+        assert (r[:, comp] == want).all()
+
+
+# ---- small primitives ----------------------------------------------------------------
+
+def test_fp2_powers_and_add(backend, oracle):
+    c = (int(P - 2), 123456789)
+    d = backend.fp2_powers_device(c, 1000)
+    got = backend.download_device(d).view(np.uint64).reshape(-1, 2)
+    assert (got == oracle.fp2_powers(c, 1000)).all()
+    other = rand_fp(8, (1000, 2))
+    from volta_mi355x import FP2
+    da = backend.alloc_device(1000, FP2)
+    backend.upload_into(da, 0, other.reshape(-1))
+    backend.fp2_add_inplace_device(d, 10, da, 20, 500)
+    after = backend.download_device(d).view(np.uint64).reshape(-1, 2)
+    backend.free_device(d)
+    backend.free_device(da)
+    want = got.copy()
+    want[10:510] = oracle.fp2_add_inplace(got[10:510], other[20:520])
+    assert (after == want).all()
+
+
+def test_gather_columns_device_and_host(backend, oracle):
+    rows, cols = 64, 1 << 12
+    m = rand_fp(9, (rows, cols))
+    idx = np.random.Generator(np.random.PCG64(3)).integers(0, cols, size=256, dtype=np.uint32)
+    dm = backend.upload_device(m.reshape(-1))
+    out = backend.pcs_gather_columns_device(dm, rows, cols, idx)
+    got = backend.download_device(out).reshape(256, rows)
+    backend.free_device(dm)
+    backend.free_device(out)
+    assert (got == oracle.gather_columns(m, idx)).all()
+    assert (backend.pcs_gather_columns(m, idx) == got).all()
+    m2 = rand_fp(10, (rows, 128, 2))
+    from volta_mi355x import FP2
+    dm2 = backend.alloc_device(rows * 128, FP2)
+    backend.upload_into(dm2, 0, m2.reshape(-1))
+    idx2 = np.array([127, 0, 5], dtype=np.uint32)
+    out2 = backend.pcs_gather_columns_device(dm2, rows, 128, idx2, fp2=True)
+    got2 = backend.download_device(out2).view(np.uint64).reshape(3, rows, 2)
+    backend.free_device(dm2)
+    backend.free_device(out2)
+    assert (got2 == oracle.gather_fp2_columns(m2, idx2)).all()
+
+
+KAT_SEED = bytes((17 * i + 3) % 256 for i in range(32))
+
+
+def test_chacha8_rows_match_fpstream_and_kat(backend, oracle):
+    # rust/volta-accel/src/lib.rs:7517-7528: the 6th raw draw of row 0 is >= p
+    d = backend.chacha8_prover_secret_fp_rows_device(KAT_SEED, 0x19664BCA, 3, 10)
+    got = backend.download_device(d).reshape(3, 10)
+    backend.free_device(d)
+    assert (got == oracle.fp_rows(KAT_SEED, 0x19664BCA, 3, 10)).all()
+    raw = oracle.raw_u64(KAT_SEED, 0x19664BCA, 8)
+    assert int(raw[5]) == 0xFFFF_FFFF_B146_1B28 and int(got[0, 5]) == int(raw[6])
+    d2 = backend.chacha8_prover_secret_fp2_rows_padded_device(KAT_SEED, 5, 4, 7, 9)
+    got2 = backend.download_device(d2).view(np.uint64).reshape(4, 9, 2)
+    backend.free_device(d2)
+    assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 5, 4, 7, 9)).all()
+
+
+def test_chacha8_rows_large(backend, oracle):
+    seed = bytes(range(32))
+    d = backend.chacha8_prover_secret_fp_rows_device(seed, 1000, 513, 512)
+    got = backend.download_device(d).reshape(513, 512)
+    backend.free_device(d)
+    assert (got == oracle.fp_rows(seed, 1000, 513, 512)).all()
+
+
+# ---- seam contract: errors and stats -------------------------------------------------
+
+def test_geometry_and_id_errors(backend):
+    from volta_mi355x import GpuError, InvalidInput
+    buf = backend.alloc_device(16, np.uint64)
+    out = backend.alloc_device(16, np.uint64)
+    lib, raw = backend.lib, backend.raw
+    assert lib.volta_cuda_ntt_fp_batch_device(raw, buf.id, 0, 1, 12, out.id, 0) != 0  # n not a power of two
+    assert "invalid resident Fp NTT geometry" in backend.last_error()
+    assert lib.volta_cuda_ntt_fp_batch_device(raw, buf.id, 0, 2, 16, out.id, 0) != 0  # region too small
+    assert "out of bounds" in backend.last_error()
+    stale = buf.id
+    backend.free_device(buf)
+    assert lib.volta_cuda_ntt_fp_batch_device(raw, stale, 0, 1, 16, out.id, 0) != 0
+    assert "unknown resident buffer id" in backend.last_error()
+    assert lib.volta_cuda_resident_free(raw, stale) != 0
+    # storage is reused under a new generation; the stale id stays invalid
+    again = backend.alloc_device(16, np.uint64)
+    assert again.id != stale
+    assert lib.volta_cuda_resident_zero(raw, stale, 0, 8) != 0
+    with pytest.raises(InvalidInput):
+        backend.pcs_messages_device(again, 0, again, 0, 1, 8, 0, 4)  # cols > code_len
+    assert lib.volta_cuda_pcs_combine_rows_device(raw, again.id, 0, again.id, 0, again.id, 0, 0, 1, 0, 1, out.id,
+                                                  0) != 0
+    # mock-correlation domains must not set the reserved bits
+    seed = (np.ctypeslib.as_ctypes(np.zeros(32, np.uint8)))
+    assert lib.volta_cuda_mock_correlation_sub_masks_device(raw, out.id, 0, seed, 1 << 61, 1, 1) != 0
+    assert "reserved correlation bits" in backend.last_error()
+    assert lib.volta_cuda_chacha8_prover_secret_fp_rows_device(raw, out.id, 0, seed, 0, 0, 1) != 0
+    # out-of-scope symbols fail explicitly
+    assert lib.volta_cuda_hash_fp_tree_device(raw, out.id, 0, 1, 16, out.id, 0) != 0
+    assert "not implemented" in backend.last_error()
+    backend.free_device(again)
+    backend.free_device(out)
+    with pytest.raises(GpuError):
+        backend._check(lib.volta_cuda_resident_free(raw, 12345))
+
+
+def test_stats_contract_of_a_cold_encode():
+    """Mirrors rust/volta-pcs/tests/cuda.rs:235-244: a cold context uploads
+    exactly the n/2 twiddle table (the only H2D besides explicit uploads) and
+    generated pads count rows*pad*8 bytes."""
+    from volta_mi355x import Backend, ligero
+    with Backend() as b:
+        rows, cols, pad, n = 16, 64, 8, 256
+        w = rand_i16(40, rows * cols)
+        dw = b.upload_device(w)
+        b.reset_stats()
+        params = ligero.LigeroParams(rows, 6, pad, 8)
+        enc, pads = ligero.commit_encode_resident(b, dw, params, pad_seed=bytes(32), fused=False)
+        s = b.get_stats()
+        assert s["h2d_bytes"] == n // 2 * 8
+        assert s["d2h_bytes"] == 0
+        assert s["device_generated_bytes"] == rows * pad * 8
+        assert s["calls"]["pcs_ntt"] == 1 and s["calls"]["pcs_rows"] == 2
+        assert s["kernel_ns"]["pcs_ntt"] > 0
+        # a second encode of the same size uploads nothing
+        b.reset_stats()
+        enc2, pads2 = ligero.commit_encode_resident(b, dw, params, pad_seed=bytes(32), fused=True)
+        s2 = b.get_stats()
+        assert s2["h2d_bytes"] == 0 and s2["calls"]["pcs_ntt"] == 1
+        assert (b.download_device(enc) == b.download_device(enc2)).all()
+        for x in (dw, enc, pads, enc2, pads2):
+            b.free_device(x)
+        live = b.get_stats()["live_device_bytes"]
+        ws, res, cached = b.memory_breakdown()
+        assert ws + res + cached == live and res == 0
+
+
+def test_coarse_timing_scope_and_wall_only_policy():
+    import ctypes
+    from volta_mi355x import Backend
+    with Backend(timing_policy=1) as b:
+        d = b.alloc_device(1 << 12, np.uint64)
+        b.reset_stats()
+        lib, raw = b.lib, b.raw
+        assert lib.volta_cuda_begin_coarse_timing(raw, 3) == 0
+        assert lib.volta_cuda_begin_coarse_timing(raw, 3) != 0  # no nesting
+        out_id = ctypes.c_uint64()
+        assert lib.volta_cuda_resident_alloc(raw, 8, ctypes.byref(out_id)) != 0
+        assert "coarse timing scope" in b.last_error()
+        assert lib.volta_cuda_end_coarse_timing(raw) == 0
+        o2 = b.ntt_fp_batch_device(d, 1, 1 << 12)
+        s = b.get_stats()
+        assert s["timing_mode"] == 4 and s["timing_event_api_calls"] == 0
+        assert s["calls"]["pcs_ntt"] == 1 and s["kernel_ns"]["pcs_ntt"] == 0
+        assert s["coarse_timing_scopes"] == 1
+        b.free_device(d)
+        b.free_device(o2)

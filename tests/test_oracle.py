@@ -16,6 +16,8 @@ import random
 import numpy as np
 import pytest
 
+import spike_inputs as spike
+
 P = 0xFFFF_FFFF_0000_0001
 EPS = 0xFFFF_FFFF
 MASK64 = (1 << 64) - 1
@@ -144,49 +146,18 @@ def test_inverse_ntt_round_trip_and_naive(oracle):
     assert naive == a[0].tolist()
 
 
-def spike_ntt_input(rows, bits, msg_len):
-    """cuda/p7_pcs_arithmetic.cu:207-211: in[idx] = (idx*0x9E3779B9 + 17) mod p
-    for j < msg_len, idx the global row-major index."""
-    n = 1 << bits
-    idx = np.arange(rows * n, dtype=np.uint64)
-    v = (idx * np.uint64(0x9E3779B9) + np.uint64(17)) % np.uint64(P)
-    v = v.reshape(rows, n)
-    v[:, msg_len:] = 0
-    return v
-
-
-@pytest.mark.parametrize("rows,bits,msg_len,expected", [
-    (32, 12, 2304, 0xA87A560725F2D016),
-    (1024, 15, 16896, 0xBE7B90425A4C7229),
-])
+@pytest.mark.parametrize("rows,bits,msg_len,expected", spike.NTT_GOLDEN)
 def test_ntt_reference_checksums(oracle, rows, bits, msg_len, expected):
-    out = oracle.ntt_forward_batch(spike_ntt_input(rows, bits, msg_len))
+    out = oracle.ntt_forward_batch(spike.ntt_input(rows, bits, msg_len))
     assert oracle.fnv(out) == expected
 
 
-def spike_combine_inputs(rows, cols):
-    """cuda/p7_pcs_arithmetic.cu:270-275."""
-    i = np.arange(rows * cols, dtype=np.uint64)
-    w = ((i * np.uint64(0x85EBCA6B) + np.uint64(29)) % np.uint64(P)).reshape(rows, cols)
-    r = np.arange(rows, dtype=np.uint64)
-    q = np.stack([(r * np.uint64(37) + np.uint64(11)) % np.uint64(P), (r * np.uint64(53) + np.uint64(5)) % np.uint64(P)], 1)
-    c = np.stack([(r * np.uint64(71) + np.uint64(7)) % np.uint64(P), (r * np.uint64(97) + np.uint64(13)) % np.uint64(P)], 1)
-    return w, q, c
-
-
-def combine_checksum(oracle, uq, uc):
-    return oracle.fnv(uq) ^ ((oracle.fnv(uc) * 0x9E3779B97F4A7C15) & MASK64)
-
-
-@pytest.mark.parametrize("rows,cols,expected", [
-    (32, 2048, 0x0852323A5805ED2C),
-    (1024, 16384, 0x856F9A96D8E01901),
-])
+@pytest.mark.parametrize("rows,cols,expected", spike.COMBINE_GOLDEN)
 def test_combination_reference_checksums(oracle, rows, cols, expected):
-    w, q, c = spike_combine_inputs(rows, cols)
+    w, q, c = spike.combine_inputs(rows, cols)
     coeffs = np.concatenate([q, c]).reshape(2 * rows, 2)
     u = oracle.combine_rows_fp(w, coeffs, 2)
-    assert combine_checksum(oracle, u[0], u[1]) == expected
+    assert spike.combine_checksum(oracle.fnv, u[0], u[1]) == expected
 
 
 def test_combination_brute_force_i16_with_pads(oracle):
@@ -213,25 +184,16 @@ def test_messages_lift_and_layout(oracle):
     assert m.tolist() == [[0, P - 1, 11, 0], [32767, P - 32768, 12, 0]]
 
 
-@pytest.mark.parametrize("log2,expected", [(20, 0xAB1B94B1D98FD160), (24, 0x33EB029C2CCB481F)])
+@pytest.mark.parametrize("log2,expected", spike.FP2_STREAM_GOLDEN)
 def test_fp2_stream_reference_checksums(oracle, log2, expected):
-    a, b = spike_fp2_inputs(1 << log2)
+    a, b = spike.fp2_inputs(1 << log2)
     assert oracle.fnv(oracle.fp2_mul_stream(a, b)) == expected
 
 
-@pytest.mark.parametrize("log2,rounds,expected", [(16, 64, 0x994B7AB598EDF5D0), (20, 256, 0x2D1768754CF29569)])
+@pytest.mark.parametrize("log2,rounds,expected", spike.FP2_CHAIN_GOLDEN)
 def test_fp2_chain_reference_checksums(oracle, log2, rounds, expected):
-    a, b = spike_fp2_inputs(1 << log2)
+    a, b = spike.fp2_inputs(1 << log2)
     assert oracle.fnv(oracle.fp2_chain(a, b, rounds)) == expected
-
-
-def spike_fp2_inputs(n):
-    """cuda/p7_goldilocks_roofline.cu:112-119."""
-    x = np.arange(n, dtype=np.uint64)
-    Pu = np.uint64(P)
-    a = np.stack([(x * np.uint64(0x9E3779B9) + np.uint64(17)) % Pu, (x * np.uint64(0x85EBCA6B) + np.uint64(29)) % Pu], 1)
-    b = np.stack([(x * np.uint64(0xC2B2AE35) + np.uint64(31)) % Pu, (x * np.uint64(0x27D4EB2F) + np.uint64(43)) % Pu], 1)
-    return a, b
 
 
 # ---- FpStream / ChaCha8 ---------------------------------------------------------------
