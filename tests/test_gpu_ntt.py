@@ -152,7 +152,10 @@ def test_compact_encode_device(backend, oracle):
 # ---- PCS encode of i16 message rows ---------------------------------------------------
 
 @pytest.mark.parametrize("rows,cols,pad,bits", [(5, 16, 0, 6), (9, 100, 7, 8), (17, 2048, 0, 13), (4, 2048, 512, 13),
-                                                (3, 4096, 0, 14), (2, 1024, 3, 15)])
+                                                (3, 4096, 0, 14), (2, 1024, 3, 15),
+                                                # the n = 2^13 fast path: full, partial and 1-column rows
+                                                (3, 1, 0, 13), (5, 1000, 0, 13), (64, 2047, 0, 13),
+                                                (1000, 2048, 0, 13)])
 def test_pcs_encode_fused_and_chain_match_oracle(backend, oracle, rows, cols, pad, bits):
     n = 1 << bits
     g = np.random.Generator(np.random.PCG64(rows * 1000 + cols))

@@ -222,6 +222,19 @@ int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** ou
     return 0;
 }
 
+int ensure_grid_twiddles(Context* c, TwiddleSet* t, size_t bytes, int (*build)(Context*, TwiddleSet*)) {
+    if (t->grid) return 0;
+    if (c->coarse_active) return reject(c, "twiddle table growth is forbidden inside a coarse timing scope");
+    void* p = nullptr;
+    VMX_HIP(c, hipMalloc(&p, bytes));
+    ++c->stats.allocation_calls;
+    c->stats.live_device_bytes += bytes;
+    c->stats.peak_device_bytes = std::max(c->stats.peak_device_bytes, c->stats.live_device_bytes);
+    t->grid = static_cast<uint64_t*>(p);
+    t->grid_bytes = bytes;
+    return build(c, t);
+}
+
 // ---- events --------------------------------------------------------------------------
 
 static hipError_t ev_create(Context* c, hipEvent_t* e) {
@@ -575,7 +588,7 @@ static int trim_pinned(Context* c) {
     for (size_t s : c->free_pinned) {
         Pinned& p = c->pinned[s];
         if (!p.ptr) continue;
-        if (p.ready) hipEventDestroy(p.ready);
+        if (p.ready) (void)hipEventDestroy(p.ready);
         p.ready = nullptr;
         VMX_HIP(c, hipHostFree(p.ptr));
         ++c->stats.pinned_physical_free_calls;
@@ -658,6 +671,7 @@ VMX_API void volta_cuda_destroy(void* raw) {
         for (auto& kv : c->twiddles) {
             if (kv.second.fwd) (void)hipFree(kv.second.fwd);
             if (kv.second.inv) (void)hipFree(kv.second.inv);
+            if (kv.second.grid) (void)hipFree(kv.second.grid);
         }
         for (auto& p : c->pinned) {
             if (p.ready) (void)hipEventDestroy(p.ready);
@@ -856,6 +870,7 @@ VMX_API int volta_cuda_memory_breakdown(void* raw, uint64_t* workspace, uint64_t
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) w += half;
         if (kv.second.inv) w += half;
+        w += kv.second.grid_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;
@@ -1228,6 +1243,7 @@ VMX_API int volta_cuda_x4c_control_state(void* raw, RawX4cControlState* out) {
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) r.workspace_device_bytes += half;
         if (kv.second.inv) r.workspace_device_bytes += half;
+        r.workspace_device_bytes += kv.second.grid_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;

@@ -184,6 +184,8 @@ struct TimingRecord {
 struct TwiddleSet {
     uint64_t* fwd = nullptr;  // w^0 .. w^(n/2-1), the reference's table
     uint64_t* inv = nullptr;  // w^0 .. w^-(n/2-1) (inverse transform only)
+    uint64_t* grid = nullptr; // w^(i2*j1) laid out for the fast encode (device-built)
+    size_t grid_bytes = 0;
     size_t n = 0;
 };
 
@@ -255,6 +257,9 @@ T* ws(Context* c, int slot) {
 // bytes to *h2d (the reference's per-size upload, .cu:2675-2689).
 int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
 int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
+// Device-built table of `bytes` for the fast encode, derived from t->fwd on
+// the device (no host upload).  `build` enqueues the kernel that fills it.
+int ensure_grid_twiddles(Context* c, TwiddleSet* t, size_t bytes, int (*build)(Context*, TwiddleSet*));
 
 // ---- timing/accounting (one primitive = begin, [mark1], [mark2], finish) ---------
 int begin_op(Context* c);

@@ -68,6 +68,20 @@ __host__ __device__ __forceinline__ uint64_t mul(uint64_t a, uint64_t b) {
     return fold128(lo, hi);
 }
 
+// The same product from four 32x32->64 partial products, each of which maps
+// onto one v_mad_u64_u32 on gfx950 (no carries can overflow: every partial
+// sum stays below 2^64).
+__host__ __device__ __forceinline__ uint64_t mul32x4(uint64_t a, uint64_t b) {
+    const uint32_t a0 = static_cast<uint32_t>(a), a1 = static_cast<uint32_t>(a >> 32);
+    const uint32_t b0 = static_cast<uint32_t>(b), b1 = static_cast<uint32_t>(b >> 32);
+    const uint64_t p00 = static_cast<uint64_t>(a0) * b0;
+    const uint64_t p01 = static_cast<uint64_t>(a0) * b1 + (p00 >> 32);
+    const uint64_t p10 = static_cast<uint64_t>(a1) * b0 + static_cast<uint32_t>(p01);
+    const uint64_t hi = static_cast<uint64_t>(a1) * b1 + (p01 >> 32) + (p10 >> 32);
+    const uint64_t lo = (p10 << 32) | static_cast<uint32_t>(p00);
+    return fold128(lo, hi);
+}
+
 inline uint64_t pow_host(uint64_t a, uint64_t e) {
     uint64_t acc = 1;
     while (e) {

@@ -27,7 +27,7 @@ int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t 
 // Fast path for the Ligero shapes (i16 messages with rate <= 1/2 and
 // n in [2^11, 2^14]); returns 1 when the shape is not covered.
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
-                    const uint64_t* tw);
+                    TwiddleSet* t);
 
 int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
                  size_t code_len, uint64_t* out);

@@ -228,7 +228,6 @@ static int ilog2(size_t n) {
 }
 
 constexpr int LDS_MAX_BITS = 14;           // 128 KiB of u64 per workgroup
-constexpr size_t LDS_MAX_WORDS = size_t{1} << LDS_MAX_BITS;
 
 template <class K>
 static hipError_t allow_lds(K kernel, size_t bytes) {

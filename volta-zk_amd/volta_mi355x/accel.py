@@ -129,6 +129,11 @@ _SIGS = {
     "volta_cuda_pcs_gather_columns": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "volta_cuda_chacha8_prover_secret_fp_rows_device": (_int, [_vp, _u64, _sz, _vp, _u64, _sz, _sz]),
     "volta_cuda_chacha8_prover_secret_fp2_rows_padded_device": (_int, [_vp, _u64, _sz, _vp, _u64, _sz, _sz, _sz]),
+    "volta_cuda_mock_correlation_sub_masks_device": (_int, [_vp, _u64, _sz, _vp, _u64, _sz, _sz]),
+    "volta_cuda_hash_fp_tree_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
+    "volta_cuda_hash_fp2_tree_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
+    "volta_cuda_merkle_paths_device": (_int, [_vp, _u64, _sz, _sz, _u64, _sz, _sz, _u64, _sz]),
+    "volta_cuda_hash_fp_columns": (_int, [_vp, _vp, _sz, _sz, _vp]),
     "volta_mi355x_ntt_fp_inverse_batch_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_ntt_fp_encode_device": (_int, [_vp, _u64, _sz, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_pcs_encode_device": (_int, [_vp, _u64, _sz, _u64, _sz, _sz, _sz, _sz, _sz, _u64, _sz]),
