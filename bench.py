@@ -208,9 +208,10 @@ def traffic_for(name: str):
     if not f.exists():
         return None
     try:
-        return json.loads(f.read_text()).get(name)
+        entry = json.loads(f.read_text()).get(name)
     except (ValueError, OSError):
         return None
+    return entry.get("bytes") if isinstance(entry, dict) else None
 
 
 def main() -> int:
