@@ -1,0 +1,74 @@
+"""The compile-time shift arithmetic of the fast encode kernels
+(volta-zk_amd/csrc/gl64_shift.hpp), built for the host from the same headers
+(libgl64_check.so), checked against Python big integers for every exponent
+and boundary inputs.  CPU only."""
+import ctypes
+import pathlib
+import random
+
+import pytest
+
+P = 0xFFFF_FFFF_0000_0001
+LIB = pathlib.Path(__file__).resolve().parent.parent / "volta-zk_amd" / "libgl64_check.so"
+
+
+@pytest.fixture(scope="module")
+def glc():
+    if not LIB.exists():
+        pytest.fail("libgl64_check.so missing: run volta-zk_amd/build.py (or __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB))
+    u64, i32 = ctypes.c_uint64, ctypes.c_int32
+    for name, res, args in [("glc_mul_pow2", u64, [u64, ctypes.c_int]), ("glc_i16_mul_w128", u64, [i32, ctypes.c_int]),
+                            ("glc_i16_mul_pow2", u64, [i32, ctypes.c_int]), ("glc_mul32x4", u64, [u64, u64]),
+                            ("glc_add", u64, [u64, u64]), ("glc_sub", u64, [u64, u64]),
+                            ("glc_bfly", None, [ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.c_int])]:
+        f = getattr(L, name)
+        f.restype, f.argtypes = res, args
+    return L
+
+
+EDGE = [0, 1, 2, 0xFFFFFFFF, 0x100000000, 0x100000001, P - 1, P - 2, P - 0xFFFFFFFF, (1 << 63), (1 << 63) + 12345,
+        0xFFFFFFFE00000002, 0x8000000080000000]
+
+
+def samples(seed, n=40):
+    rnd = random.Random(seed)
+    return EDGE + [rnd.randrange(P) for _ in range(n)]
+
+
+def test_mul_pow2_every_exponent(glc):
+    for e in range(192):
+        w = pow(2, e, P)
+        for x in samples(e):
+            assert glc.glc_mul_pow2(x, e) == x * w % P, (e, x)
+
+
+def test_butterfly_every_exponent(glc):
+    for e in range(192):
+        w = pow(2, e, P)
+        for x in samples(1000 + e, 10):
+            u, v = ctypes.c_uint64(x), ctypes.c_uint64((x * 7 + 3) % P)
+            a, b = u.value, v.value
+            glc.glc_bfly(ctypes.byref(u), ctypes.byref(v), e)
+            assert (u.value, v.value) == ((a + w * b) % P, (a - w * b) % P), (e, a, b)
+
+
+def test_i16_pre_twiddles(glc):
+    w128 = pow(7, (P - 1) >> 7, P)
+    xs = [0, 1, -1, 32767, -32768, 12345, -23456]
+    for k in range(128):
+        for x in xs:
+            assert glc.glc_i16_mul_w128(x, k) == x * pow(w128, k, P) % P, (k, x)
+    for e in range(192):
+        for x in xs:
+            assert glc.glc_i16_mul_pow2(x, e) == x * pow(2, e, P) % P, (e, x)
+
+
+def test_general_mul_add_sub(glc):
+    rnd = random.Random(3)
+    vals = EDGE + [rnd.randrange(P) for _ in range(300)]
+    for a in vals:
+        b = rnd.choice(vals)
+        assert glc.glc_mul32x4(a, b) == a * b % P
+        assert glc.glc_add(a, b) == (a + b) % P
+        assert glc.glc_sub(a, b) == (a - b) % P

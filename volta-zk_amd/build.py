@@ -20,6 +20,8 @@ HERE = pathlib.Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "libvolta_mi355x_backend.so"
+# Host build of the device arithmetic headers for the CPU tests (not shipped).
+CHECK_LIB = HERE / "libgl64_check.so"
 SOURCES = ["context.cpp", "ntt.hip", "encode_fast.hip", "pcs.hip", "abi_pcs.cpp", "abi_stubs.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -55,6 +57,13 @@ def build(jobs: int | None = None) -> pathlib.Path:
         sys.stderr.write(r.stdout + r.stderr)
         raise RuntimeError("link failed")
     os.replace(tmp, LIB)
+    # host-only compile of the same headers: no device code in this library
+    cmd = [HIPCC, "-x", "hip", "--cuda-host-only", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-I", str(CSRC), str(CSRC / "host_check.cpp"), "-o", str(CHECK_LIB)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError("host check library failed to build")
     return LIB
 
 

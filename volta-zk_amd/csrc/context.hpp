@@ -166,6 +166,7 @@ enum WorkspaceSlot : int {
     WS_AUX1 = 3,
     WS_PARTIALS = 4,  // combination partial sums
     WS_TRANSPOSE = 5, // four-step intermediate
+    WS_AUX2 = 6,      // combination coefficient sums
     WS_COUNT = 8,
 };
 

@@ -21,18 +21,29 @@ constexpr uint64_t EPS = 0x00000000FFFFFFFFull;
 
 __host__ __device__ __forceinline__ uint64_t canon(uint64_t x) { return x >= P ? x - P : x; }
 
+// s = a + b; the result is s - p exactly when a + b >= p, i.e. when the sum
+// carries out of 64 bits or s + eps does (s >= 2^64 - eps = p); s - p is then
+// s + eps mod 2^64.  Written on 32-bit carry chains (v_add_co/v_addc).
 __host__ __device__ __forceinline__ uint64_t add(uint64_t a, uint64_t b) {
-    uint64_t r = a + b;
-    // A carry out of 2^64 is worth eps; with a, b < p the corrected value
-    // stays below 2^64.
-    r += (r < a) ? EPS : 0;
-    return r >= P ? r - P : r;
+    unsigned c0, c1, d0, d1;
+    const uint32_t s0 = __builtin_addc(static_cast<uint32_t>(a), static_cast<uint32_t>(b), 0u, &c0);
+    const uint32_t s1 = __builtin_addc(static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32), c0, &c1);
+    const uint32_t t0 = __builtin_addc(s0, 0xFFFFFFFFu, 0u, &d0);
+    const uint32_t t1 = __builtin_addc(s1, 0u, d0, &d1);
+    const bool over = (c1 | d1) != 0;
+    return (static_cast<uint64_t>(over ? t1 : s1) << 32) | (over ? t0 : s0);
 }
 
+// d = a - b; a borrow out of 64 bits is worth -2^64 = -eps, i.e. d - eps,
+// which stays >= 0 for canonical inputs.
 __host__ __device__ __forceinline__ uint64_t sub(uint64_t a, uint64_t b) {
-    uint64_t r = a - b;
-    // A borrow is worth -2^64 = -eps; with a, b < p the result stays >= 0.
-    return (a < b) ? r - EPS : r;
+    unsigned b0, b1, e0;
+    const uint32_t d0 = __builtin_subc(static_cast<uint32_t>(a), static_cast<uint32_t>(b), 0u, &b0);
+    const uint32_t d1 = __builtin_subc(static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32), b0, &b1);
+    const uint32_t e = b1 ? 0xFFFFFFFFu : 0u;
+    const uint32_t r0 = __builtin_subc(d0, e, 0u, &e0);
+    const uint32_t r1 = d1 - e0;
+    return (static_cast<uint64_t>(r1) << 32) | r0;
 }
 
 __host__ __device__ __forceinline__ uint64_t neg(uint64_t a) { return a ? P - a : 0; }

@@ -21,23 +21,69 @@ namespace gl {
 constexpr int E_W64 = 39;  // w_64 = 2^39
 constexpr int E_W32 = 78;  // w_32 = 2^78
 
+// x * 2^-M mod p for 1 <= M <= 32, x canonical; canonical result.
+// With x = q 2^M + r (r < 2^M): x 2^-M = q + r 2^-M and 2^-M = -2^(96-M), so
+// x 2^-M = q - r 2^(32-M) 2^64 = q - r' eps with r' = r 2^(32-M) < 2^32; both
+// q < 2^(64-M) and r' eps <= (2^32-1)^2 are canonical.
+template <int M>
+__host__ __device__ __forceinline__ uint64_t shr_mod(uint64_t x) {
+    static_assert(M >= 1 && M <= 32, "shift out of range");
+    const uint64_t q = x >> M;
+    const uint32_t rp = static_cast<uint32_t>(x) << (32 - M);
+    return sub(q, static_cast<uint64_t>(rp) * EPS);
+}
+
+// x * 2^(32+SM) mod p for 0 <= SM < 32, x canonical; canonical result.
+// In 32-bit words x 2^SM = W1 + W2 2^32 + W3 2^64, so x 2^(32+SM) =
+// W1 2^32 + W2 2^64 + W3 2^96 = (W1 + W2) 2^32 - (W2 + W3)  (2^64 = 2^32 - 1,
+// 2^96 = -1): two 32-bit sums and one borrow-corrected 64-bit difference.
+template <int SM>
+__host__ __device__ __forceinline__ uint64_t shl_mod_hi(uint64_t x) {
+    static_assert(SM >= 0 && SM < 32, "shift out of range");
+    const uint32_t x0 = static_cast<uint32_t>(x), x1 = static_cast<uint32_t>(x >> 32);
+    uint32_t w1, w2, w3;
+    if constexpr (SM == 0) {
+        w1 = x0;
+        w2 = x1;
+        w3 = 0;
+    } else {
+        w1 = x0 << SM;
+        w2 = (x1 << SM) | (x0 >> (32 - SM));
+        w3 = x1 >> (32 - SM);
+    }
+    unsigned ca, cb, c2, b0, b1;
+    const uint32_t a = __builtin_addc(w1, w2, 0u, &ca);  // A = a + ca 2^32
+    const uint32_t b = __builtin_addc(w2, w3, 0u, &cb);  // B = b + cb 2^32 < 2^32 + 2^31
+    const uint32_t h = a + ca;                           // A 2^32 = (a + ca) 2^32 - ca
+    const uint32_t clo = __builtin_addc(b, 0u, ca, &c2); // C = B + ca = clo + chi 2^32
+    const uint32_t chi = cb | c2;
+    const uint32_t r0 = __builtin_subc(0u, clo, 0u, &b0);  // r = h 2^32 - C
+    const uint32_t r1 = __builtin_subc(h, chi, b0, &b1);
+    const uint64_t r = (static_cast<uint64_t>(r1) << 32) | r0;
+    return b1 ? r - EPS : r;  // negative: + p = - eps mod 2^64
+}
+
 // x * 2^S mod p for 0 <= S < 96, x canonical; canonical result.
 template <int S>
 __host__ __device__ __forceinline__ uint64_t shl_mod(uint64_t x) {
     static_assert(S >= 0 && S < 96, "shift out of range");
     if constexpr (S == 0) {
         return x;
-    } else if constexpr (S < 64) {
+    } else if constexpr (S < 32) {
         return fold128(x << S, x >> (64 - S));
-    } else if constexpr (S == 64) {
-        return fold128(0, x);
+    } else if constexpr (S < 64) {
+        return shl_mod_hi<S - 32>(x);
     } else {
-        // x*2^S = y*2^64 with y = x*2^(S-64) = yhi*2^64 + ylo, yhi < 2^32;
-        // y*2^64 = ylo*2^64 + yhi*2^128 = ylo*eps - yhi*2^32 (2^128 = -2^32).
-        const uint64_t ylo = x << (S - 64);
-        const uint64_t yhi = x >> (128 - S);
-        return sub(fold128(0, ylo), yhi << 32);  // yhi << 32 <= 2^64 - 2^32 < p
+        // 2^S = -2^-(96-S): one division by a power of two <= 2^32.
+        return neg(shr_mod<96 - S>(x));
     }
+}
+
+// -(x * 2^S) mod p for 64 <= S < 96 without the final negation.
+template <int S>
+__host__ __device__ __forceinline__ uint64_t shl_mod_neg(uint64_t x) {
+    static_assert(S >= 64 && S < 96, "only the division form has a cheap negative");
+    return shr_mod<96 - S>(x);
 }
 
 // x * 2^E mod p for any E >= 0 (reduced mod 192; E mod 192 >= 96 negates).
@@ -60,17 +106,29 @@ __host__ __device__ __forceinline__ void bfly_pow2(uint64_t& u, uint64_t& v) {
         const uint64_t a = sub(u, v), b = add(u, v);
         u = a;
         v = b;
-    } else if constexpr (e < 96) {
-        const uint64_t t = shl_mod<e>(v);
-        const uint64_t a = add(u, t), b = sub(u, t);
-        u = a;
-        v = b;
     } else {
-        // w = -2^(e-96): swap the roles of sum and difference
-        const uint64_t t = shl_mod<e - 96>(v);
-        const uint64_t a = sub(u, t), b = add(u, t);
-        u = a;
-        v = b;
+        // w = +-2^S with S = e mod 96; for S >= 64 the division form yields
+        // -(v 2^S) directly, which flips the sign once more.
+        constexpr int S = e % 96;
+        constexpr bool neg_w = e >= 96;
+        uint64_t t;
+        bool neg_t;
+        if constexpr (S >= 64) {
+            t = shl_mod_neg<S>(v);
+            neg_t = !neg_w;
+        } else {
+            t = shl_mod<S>(v);
+            neg_t = neg_w;
+        }
+        if (neg_t) {
+            const uint64_t a = sub(u, t), b = add(u, t);
+            u = a;
+            v = b;
+        } else {
+            const uint64_t a = add(u, t), b = sub(u, t);
+            u = a;
+            v = b;
+        }
     }
 }
 

@@ -56,15 +56,55 @@ int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows
 // - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
 // absorb up to 2^16 rows exactly; the fold to a field element happens once.
 
-constexpr int COMB_COLS = 4;      // columns per thread (one 8-byte i16 load)
+constexpr int COMB_COLS = 4;       // columns per thread (one 8-byte i16 load)
 constexpr int COMB_THREADS = 256;
-constexpr size_t COMB_CHUNK = 128; // rows per partial
+constexpr size_t COMB_CHUNK = 256;  // rows per partial
+constexpr int COMB_UNROLL = 8;      // row loads kept in flight per thread
 
+// S[ck][comb][h] = sum over the chunk's rows of component h of coeff[comb][i]
+// (mod p): the 2^15 bias correction of the offset-binary trick below.
+__global__ __launch_bounds__(256) void coeff_chunk_sums(const Fp2* coeffs, uint64_t* sums, size_t rows,
+                                                        size_t chunk) {
+    __shared__ uint64_t red[4][256];
+    const size_t ck = blockIdx.x, comb = blockIdx.y, combinations = gridDim.y;
+    const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
+    uint64_t lo0 = 0, hi0 = 0, lo1 = 0, hi1 = 0;  // 32-bit halves summed exactly
+    for (size_t i = r0 + threadIdx.x; i < r1; i += blockDim.x) {
+        const Fp2 cf = coeffs[comb * rows + i];
+        lo0 += static_cast<uint32_t>(cf.c0);
+        hi0 += cf.c0 >> 32;
+        lo1 += static_cast<uint32_t>(cf.c1);
+        hi1 += cf.c1 >> 32;
+    }
+    red[0][threadIdx.x] = lo0;
+    red[1][threadIdx.x] = hi0;
+    red[2][threadIdx.x] = lo1;
+    red[3][threadIdx.x] = hi1;
+    __syncthreads();
+    for (int w = blockDim.x / 2; w > 0; w >>= 1) {
+        if (static_cast<int>(threadIdx.x) < w)
+            for (int q = 0; q < 4; ++q) red[q][threadIdx.x] += red[q][threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const uint64_t two32 = 0x100000000ull;
+        // chunk <= 2^16 rows keeps each half-sum below 2^48
+        sums[(ck * combinations + comb) * 2 + 0] = gl::add(gl::canon(red[0][0]), gl::mul(gl::canon(red[1][0]), two32));
+        sums[(ck * combinations + comb) * 2 + 1] = gl::add(gl::canon(red[2][0]), gl::mul(gl::canon(red[3][0]), two32));
+    }
+}
+
+// out[comb][j] = sum_i coeff[comb][i] * msg_i[j] (reference combine_row_range,
+// rust/volta-pcs/src/ligero.rs:1114-1135) for KC combinations at once.
+// i16 data: with w' = w + 2^15 in [0, 2^16) and a coefficient component
+// x = xh*2^32 + xl, sum_i x_i w_i = sum xl_i w'_i + 2^32 sum xh_i w'_i
+// - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
+// absorb up to 2^16 rows exactly; the fold to a field element happens once.
 template <int KC>
 __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_t* w, const Fp2* coeffs,
-                                                                   Fp2* partials, size_t rows, size_t cols,
-                                                                   size_t msg_len, size_t comb0,
-                                                                   size_t combinations, size_t chunk,
+                                                                   const uint64_t* sums, Fp2* partials,
+                                                                   size_t rows, size_t cols, size_t msg_len,
+                                                                   size_t comb0, size_t combinations, size_t chunk,
                                                                    int vec_ok) {
     const size_t j0 = (static_cast<size_t>(blockIdx.x) * COMB_THREADS + threadIdx.x) * COMB_COLS;
     const size_t ck = blockIdx.y;
@@ -72,16 +112,15 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
     const size_t r1 = min(rows, r0 + chunk);
     uint64_t acc_lo[KC][2][COMB_COLS] = {};
     uint64_t acc_hi[KC][2][COMB_COLS] = {};
-    uint64_t s_lo[KC][2] = {}, s_hi[KC][2] = {};
-    const bool full = j0 + COMB_COLS <= cols;
-    for (size_t i = r0; i < r1; ++i) {
-        uint32_t wp[COMB_COLS];
-        if (full && vec_ok) {
-            const uint2 raw = *reinterpret_cast<const uint2*>(w + i * cols + j0);
-            wp[0] = (raw.x & 0xFFFFu) ^ 0x8000u;
-            wp[1] = (raw.x >> 16) ^ 0x8000u;
-            wp[2] = (raw.y & 0xFFFFu) ^ 0x8000u;
-            wp[3] = (raw.y >> 16) ^ 0x8000u;
+    const bool fast = (j0 + COMB_COLS <= cols) && vec_ok;
+    auto load = [&](size_t i, uint32_t* wp) {
+        if (fast) {
+            const uint64_t raw = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(w + i * cols + j0));
+            const uint32_t rx = static_cast<uint32_t>(raw), ry = static_cast<uint32_t>(raw >> 32);
+            wp[0] = (rx & 0xFFFFu) ^ 0x8000u;
+            wp[1] = (rx >> 16) ^ 0x8000u;
+            wp[2] = (ry & 0xFFFFu) ^ 0x8000u;
+            wp[3] = (ry >> 16) ^ 0x8000u;
         } else {
 #pragma unroll
             for (int q = 0; q < COMB_COLS; ++q) {
@@ -89,6 +128,8 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
                 wp[q] = j < cols ? (static_cast<uint32_t>(static_cast<uint16_t>(w[i * cols + j])) ^ 0x8000u) : 0x8000u;
             }
         }
+    };
+    auto accumulate = [&](size_t i, const uint32_t* wp) {
 #pragma unroll
         for (int k = 0; k < KC; ++k) {
             const Fp2 cf = coeffs[(comb0 + k) * rows + i];
@@ -97,8 +138,6 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
             for (int h = 0; h < 2; ++h) {
                 const uint32_t xl = static_cast<uint32_t>(comp[h]);
                 const uint32_t xh = static_cast<uint32_t>(comp[h] >> 32);
-                s_lo[k][h] += xl;
-                s_hi[k][h] += xh;
 #pragma unroll
                 for (int q = 0; q < COMB_COLS; ++q) {
                     acc_lo[k][h][q] += static_cast<uint64_t>(xl) * wp[q];
@@ -106,6 +145,19 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
                 }
             }
         }
+    };
+    size_t i = r0;
+    for (; i + COMB_UNROLL <= r1; i += COMB_UNROLL) {
+        uint32_t wp[COMB_UNROLL][COMB_COLS];
+#pragma unroll
+        for (int u = 0; u < COMB_UNROLL; ++u) load(i + u, wp[u]);
+#pragma unroll
+        for (int u = 0; u < COMB_UNROLL; ++u) accumulate(i + u, wp[u]);
+    }
+    for (; i < r1; ++i) {
+        uint32_t wp[COMB_COLS];
+        load(i, wp);
+        accumulate(i, wp);
     }
     const uint64_t two32 = 0x100000000ull;
 #pragma unroll
@@ -113,11 +165,7 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
         if (comb0 + k >= combinations) break;
         uint64_t bias[2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // 2^15 * sum x_i  (mod p)
-            const uint64_t sx = gl::add(gl::canon(s_lo[k][h]), gl::mul(gl::canon(s_hi[k][h]), two32));
-            bias[h] = gl::mul(sx, 0x8000ull);
-        }
+        for (int h = 0; h < 2; ++h) bias[h] = gl::mul(sums[(ck * combinations + comb0 + k) * 2 + h], 0x8000ull);
 #pragma unroll
         for (int q = 0; q < COMB_COLS; ++q) {
             const size_t j = j0 + q;
@@ -203,13 +251,26 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_fp_partial(const uint64_
     }
 }
 
-__global__ void reduce_partials(const Fp2* partials, Fp2* out, size_t chunks, size_t per_chunk) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < per_chunk; z += stride) {
-        Fp2 acc{0, 0};
-        for (size_t ck = 0; ck < chunks; ++ck) acc = gl::fp2_add(acc, partials[ck * per_chunk + z]);
-        out[z] = acc;
+// out[z] = sum over chunks of partials[ck][z]: 64 outputs x 16 chunk lanes per
+// workgroup, then a tree over the lanes in LDS.
+constexpr int RED_Z = 64;
+constexpr int RED_LANES = 16;
+
+__global__ __launch_bounds__(RED_Z * RED_LANES) void reduce_partials(const Fp2* partials, Fp2* out, size_t chunks,
+                                                                     size_t per_chunk) {
+    __shared__ Fp2 red[RED_LANES][RED_Z];
+    const int tz = threadIdx.x % RED_Z, tl = threadIdx.x / RED_Z;
+    const size_t z = static_cast<size_t>(blockIdx.x) * RED_Z + tz;
+    Fp2 acc{0, 0};
+    if (z < per_chunk)
+        for (size_t ck = tl; ck < chunks; ck += RED_LANES) acc = gl::fp2_add(acc, partials[ck * per_chunk + z]);
+    red[tl][tz] = acc;
+    __syncthreads();
+    for (int w = RED_LANES / 2; w > 0; w >>= 1) {
+        if (tl < w) red[tl][tz] = gl::fp2_add(red[tl][tz], red[tl + w][tz]);
+        __syncthreads();
     }
+    if (tl == 0 && z < per_chunk) out[z] = red[0][tz];
 }
 
 template <class F>
@@ -227,12 +288,18 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
                      size_t cols, size_t pad, size_t combinations, Fp2* out) {
     const size_t msg_len = cols + pad;
     const size_t chunks = (rows + COMB_CHUNK - 1) / COMB_CHUNK;
-    size_t per_chunk = 0, bytes = 0;
-    if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes))
+    size_t per_chunk = 0, bytes = 0, sum_bytes = 0;
+    if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes) ||
+        !mul_ok(chunks * combinations, 2 * sizeof(uint64_t), &sum_bytes))
         return fail_msg(c, "PCS combination partials overflow size_t");
-    if (chunks > 65535) return fail_msg(c, "PCS combination row count exceeds the supported maximum");
-    if (ensure_ws(c, WS_PARTIALS, bytes)) return -1;
+    if (chunks > 65535 || combinations > 65535)
+        return fail_msg(c, "PCS combination row or combination count exceeds the supported maximum");
+    if (ensure_ws(c, WS_PARTIALS, bytes) || ensure_ws(c, WS_AUX2, sum_bytes)) return -1;
     Fp2* part = ws<Fp2>(c, WS_PARTIALS);
+    uint64_t* sums = ws<uint64_t>(c, WS_AUX2);
+    hipLaunchKernelGGL(coeff_chunk_sums, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(combinations)),
+                       dim3(256), 0, c->stream, coeffs, sums, rows, COMB_CHUNK);
+    VMX_HIP(c, hipGetLastError());
     const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
     const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
                     static_cast<unsigned>(chunks));
@@ -240,11 +307,13 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
     const int vec_ok = (reinterpret_cast<uintptr_t>(w) % 8 == 0) && (cols % 4 == 0);
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
-                hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs, part,
-                                   rows, cols, msg_len, c0, combinations, COMB_CHUNK, vec_ok);
+                hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
+                                   static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
+                                   COMB_CHUNK, vec_ok);
             else
-                hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs, part,
-                                   rows, cols, msg_len, c0, combinations, COMB_CHUNK, vec_ok);
+                hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
+                                   static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
+                                   COMB_CHUNK, vec_ok);
             VMX_HIP(c, hipGetLastError());
             return 0;
         }))
@@ -257,8 +326,8 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
                            msg_len, combinations, COMB_CHUNK);
         VMX_HIP(c, hipGetLastError());
     }
-    hipLaunchKernelGGL(reduce_partials, dim3(grid_for(per_chunk, 256, 4096)), dim3(256), 0, c->stream,
-                       static_cast<const Fp2*>(part), out, chunks, per_chunk);
+    hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
+                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
@@ -286,8 +355,8 @@ int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, con
             return 0;
         }))
         return -1;
-    hipLaunchKernelGGL(reduce_partials, dim3(grid_for(per_chunk, 256, 4096)), dim3(256), 0, c->stream,
-                       static_cast<const Fp2*>(part), out, chunks, per_chunk);
+    hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
+                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
