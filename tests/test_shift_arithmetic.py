@@ -55,7 +55,8 @@ def test_butterfly_every_exponent(glc):
 
 def test_i16_pre_twiddles(glc):
     w128 = pow(7, (P - 1) >> 7, P)
-    xs = [0, 1, -1, 32767, -32768, 12345, -23456]
+    rnd = random.Random(7)
+    xs = [0, 1, -1, 2, -2, 32767, -32768, 32766, -32767, 12345, -23456] + [rnd.randrange(-32768, 32768) for _ in range(24)]
     for k in range(128):
         for x in xs:
             assert glc.glc_i16_mul_w128(x, k) == x * pow(w128, k, P) % P, (k, x)

@@ -636,6 +636,7 @@ VMX_API int volta_cuda_create(void** out) {
     if (e != hipSuccess) return fail_hip(c, "hipGetDeviceCount", e);
     if (count < 1) return fail_msg(c, "no HIP device is available");
     VMX_HIP(c, hipGetDevice(&c->device));
+    VMX_HIP(c, hipDeviceGetAttribute(&c->cu_count, hipDeviceAttributeMultiprocessorCount, c->device));
     // Default-priority non-blocking stream: all context work is ordered on it.
     VMX_HIP(c, hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     for (auto& ev : c->events) VMX_HIP(c, ev_create(c, &ev));

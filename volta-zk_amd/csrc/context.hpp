@@ -192,6 +192,7 @@ struct TwiddleSet {
 
 struct Context {
     int device = 0;
+    int cu_count = 0;  // compute units of `device` (sizes persistent grids)
     hipStream_t stream = nullptr;
     hipEvent_t events[4]{};
     std::vector<Resident> resident;

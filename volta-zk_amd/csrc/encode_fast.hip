@@ -13,11 +13,12 @@
 //     pre-twiddled inputs.  w128^k is a power of two (or a difference of two)
 //     times a 16-bit integer, w32 = 2^78: shifts only.  Then
 //       Y[j1][i2] = X[j1] * w_n^(i2 j1)      (the only 64x64 products)
-//   phase B (thread = row j1 x parity h, h = wave >> 1): the 64-point DFT over
+//   phase B (thread = row j1 x parity h, h = 1 - (wave & 1)): the 64-point DFT over
 //     i2 (w64 = 2^39) as its first radix-2 DIF stage followed by one 32-point
 //     DFT per parity; X[2k + h] goes to out[j1 + 128 (2k + h)], so each store
 //     instruction writes 64 consecutive u64.
-// One workgroup (4 waves) per row; Y lives in LDS with a padded pitch.
+// A persistent grid of 4-wave workgroups walks the rows; Y lives in LDS with a
+// padded pitch.
 // HBM traffic per row: 4 KiB of i16 read + 64 KiB of u64 written.
 #include <hip/hip_runtime.h>
 
@@ -39,18 +40,31 @@ constexpr int PITCH = 65;  // u64 per LDS row of Y
 constexpr int THREADS = 256;
 constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 
-// Phase A for coset S and column i2 of one row: writes Y[4 t1 + S][i2].
-template <int S>
-__host__ __device__ __forceinline__ void phase_a(const int16_t* wr, size_t cols, int i2, const uint64_t* grid,
-                                                 uint64_t* Y) {
-    int32_t x[K];
-    // Branchless bounds: clamp the address, zero the value past cols.
+// The 32 possibly non-zero entries x[64 i1 + i2] (i1 < 32) of one row, zero
+// past cols.  A raw buffer resource spanning exactly the row's cols entries
+// makes the hardware return 0 for the tail (an out-of-range buffer load reads
+// zero and touches no memory), and all 32 loads share one offset register.
+__device__ __forceinline__ void load_column(const int16_t* wr, size_t cols, int i2, int32_t* x) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int16_t*>(wr), static_cast<short>(0), static_cast<int>(cols * sizeof(int16_t)), 0x00020000);
+    const int off = i2 * static_cast<int>(sizeof(int16_t));
 #pragma unroll
-    for (int i1 = 0; i1 < K; ++i1) {
-        const size_t idx = static_cast<size_t>(i1) * N2 + i2;
-        const int32_t raw = static_cast<int32_t>(wr[idx < cols ? idx : cols - 1]);
-        x[i1] = idx < cols ? raw : 0;
-    }
+    for (int i1 = 0; i1 < K; ++i1)
+        x[i1] = static_cast<int16_t>(  // the builtin returns the 16 bits unsigned
+            __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + i1 * N2 * static_cast<int>(sizeof(int16_t)), 0, 0));
+}
+
+// Phase A for coset S and column i2 of one row: writes Y[4 t1 + S][i2].
+// The four-step twiddles w_n^(i2 (4 t1 + S)) come from the L2-resident grid;
+// their loads are issued before the DFT so its arithmetic covers the latency.
+template <int S>
+__host__ __device__ __forceinline__ void phase_a(const int32_t* x, const uint64_t* grid, int i2, uint64_t* Y) {
+    uint64_t g[K];
+#pragma unroll
+    for (int t1 = 0; t1 < K; ++t1) g[t1] = grid[(4 * t1 + S) * N2 + i2];
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the DFT
+#endif
     uint64_t v[K];
     gl::static_for<0, K>([&](auto ii) {
         constexpr int i1 = decltype(ii)::value;
@@ -58,10 +72,7 @@ __host__ __device__ __forceinline__ void phase_a(const int16_t* wr, size_t cols,
     });
     gl::dit_pow2<5, gl::E_W32>(v);
 #pragma unroll
-    for (int t1 = 0; t1 < K; ++t1) {
-        const int j1 = 4 * t1 + S;
-        Y[j1 * PITCH + i2] = gl::mul32x4(v[t1], grid[j1 * N2 + i2]);
-    }
+    for (int t1 = 0; t1 < K; ++t1) Y[(4 * t1 + S) * PITCH + i2] = gl::mul32x4(v[t1], g[t1]);
 }
 
 // Phase B for row j1 and output parity H: returns X[2k + H] in v[k].
@@ -77,32 +88,47 @@ __host__ __device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, uint
     gl::dit_pow2<5, gl::E_W32>(v);
 }
 
-__global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __restrict__ w, size_t cols,
+// One wave's share of every row its workgroup owns: wave S runs phase A for
+// coset S and phase B for rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and
+// parity 1 - (S & 1), so coset and parity are compile-time and no lane
+// diverges.  The even cosets (pre-twiddles are pure shifts) take the dearer
+// parity 1 (sub + shift first stage), which evens out the four waves' work
+// between the two barriers.  The workgroup walks rows blockIdx.x,
+// blockIdx.x + gridDim.x, ..., loading the next row's inputs while phase B of
+// the current row runs.
+template <int S>
+__device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_t cols, size_t rows,
+                                            const uint64_t* __restrict__ grid, uint64_t* __restrict__ out,
+                                            uint64_t* Y, int lane) {
+    constexpr int H = 1 - (S & 1);
+    const int j1 = (S >> 1) * 64 + lane;
+    int32_t x[K];
+    size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
+    load_column(w + row * cols, cols, lane, x);
+    for (; row < rows; row += gridDim.x) {
+        phase_a<S>(x, grid, lane, Y);
+        const size_t next = row + gridDim.x;
+        if (next < rows) load_column(w + next * cols, cols, lane, x);
+        __syncthreads();
+        uint64_t v[32];
+        phase_b<H>(Y, j1, v);
+        uint64_t* o = out + row * N + j1;
+#pragma unroll
+        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * (2 * k + H));
+        __syncthreads();  // Y is rewritten by the next row's phase A
+    }
+}
+
+__global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __restrict__ w, size_t cols, size_t rows,
                                                           const uint64_t* __restrict__ grid,
                                                           uint64_t* __restrict__ out) {
     extern __shared__ uint64_t Y[];
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const size_t row = blockIdx.x;
-    const int16_t* wr = w + row * cols;
-    switch (wave) {
-        case 0: phase_a<0>(wr, cols, lane, grid, Y); break;
-        case 1: phase_a<1>(wr, cols, lane, grid, Y); break;
-        case 2: phase_a<2>(wr, cols, lane, grid, Y); break;
-        default: phase_a<3>(wr, cols, lane, grid, Y); break;
-    }
-    __syncthreads();
-    const int j1 = (wave & 1) * 64 + lane;
-    uint64_t* o = out + row * N + j1;
-    uint64_t v[32];
-    if (wave < 2) {
-        phase_b<0>(Y, j1, v);
-#pragma unroll
-        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * (2 * k));
-    } else {
-        phase_b<1>(Y, j1, v);
-#pragma unroll
-        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * (2 * k + 1));
+    switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
+        case 0: encode_rows<0>(w, cols, rows, grid, out, Y, lane); break;
+        case 1: encode_rows<1>(w, cols, rows, grid, out, Y, lane); break;
+        case 2: encode_rows<2>(w, cols, rows, grid, out, Y, lane); break;
+        default: encode_rows<3>(w, cols, rows, grid, out, Y, lane); break;
     }
 }
 
@@ -128,6 +154,7 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
                     TwiddleSet* t) {
     if (n != static_cast<size_t>(enc13::N) || cols == 0 || cols > static_cast<size_t>(enc13::K * enc13::N2))
         return 1;
+    if (rows == 0) return 0;
     if (ensure_grid_twiddles(c, t, size_t{enc13::N1} * enc13::N2 * sizeof(uint64_t), enc13::build_grid)) return -1;
     static bool lds_ok = false;  // the attribute is per-process, per-kernel
     if (!lds_ok) {
@@ -136,13 +163,14 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
                                        static_cast<int>(enc13::LDS_BYTES)));
         lds_ok = true;
     }
-    for (size_t r0 = 0; r0 < rows; r0 += 0x7FFFFFFF) {
-        const size_t cnt = std::min<size_t>(rows - r0, 0x7FFFFFFF);
-        hipLaunchKernelGGL(enc13::encode13_i16, dim3(static_cast<unsigned>(cnt)), dim3(enc13::THREADS),
-                           enc13::LDS_BYTES, c->stream, w + r0 * cols, cols, static_cast<const uint64_t*>(t->grid),
-                           out + r0 * enc13::N);
-        VMX_HIP(c, hipGetLastError());
-    }
+    // Two workgroups fit a CU (LDS); a persistent grid of that many overlaps
+    // each row's input loads with the previous row's phase B.
+    const size_t per_cu = 2;
+    const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
+    const unsigned blocks = static_cast<unsigned>(std::min(rows, per_cu * cus));
+    hipLaunchKernelGGL(enc13::encode13_i16, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream, w, cols,
+                       rows, static_cast<const uint64_t*>(t->grid), out);
+    VMX_HIP(c, hipGetLastError());
     return 0;
 }
 

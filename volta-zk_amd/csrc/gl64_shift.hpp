@@ -132,6 +132,14 @@ __host__ __device__ __forceinline__ void bfly_pow2(uint64_t& u, uint64_t& v) {
     }
 }
 
+// Field element of a signed 64-bit integer y with |y| < 2^63: y, or y + p
+// for y < 0.  In two's complement y + p = (2^64 + y) - eps, and the sign word
+// y >> 63 read as an unsigned 32-bit value is eps exactly when y < 0.
+__host__ __device__ __forceinline__ uint64_t from_i64(uint64_t y) {
+    const uint32_t m = static_cast<uint32_t>(static_cast<int32_t>(static_cast<uint32_t>(y >> 32)) >> 31);
+    return y - m;
+}
+
 // Field element of a * 2^S for |a| <= 2^15 (a signed), 0 <= S < 96.
 template <int S>
 __host__ __device__ __forceinline__ uint64_t small_shl_abs(uint32_t ax) {
@@ -144,26 +152,37 @@ __host__ __device__ __forceinline__ uint64_t small_shl_abs(uint32_t ax) {
     }
 }
 
-// Field element of x * 2^E for a signed 16-bit x (any E >= 0).
+// Field element of x * 2^E for a signed 16-bit x (any E >= 0).  Up to a
+// shift of 47 the product +-x 2^s is an exact signed 64-bit integer
+// (|x| <= 2^15), so one sign fix-up replaces the modular reduction.
 template <int E>
 __host__ __device__ __forceinline__ uint64_t i16_mul_pow2(int32_t x) {
     constexpr int e = E % 192;
     constexpr bool flip = e >= 96;
-    const uint32_t ax = static_cast<uint32_t>(x < 0 ? -x : x);
-    const uint64_t m = small_shl_abs<flip ? e - 96 : e>(ax);
-    const bool negate = (x < 0) != flip;
-    return negate ? neg(m) : m;
+    constexpr int s = flip ? e - 96 : e;
+    if constexpr (s <= 47) {
+        const uint64_t v = static_cast<uint64_t>(static_cast<int64_t>(flip ? -x : x));
+        return from_i64(v << s);
+    } else {
+        const uint32_t ax = static_cast<uint32_t>(x < 0 ? -x : x);
+        const uint64_t m = small_shl_abs<s>(ax);
+        const bool negate = (x < 0) != flip;
+        return negate ? neg(m) : m;
+    }
 }
 
 // Field element of x * w_128^k for a signed 16-bit x: w_128^k = 2^(39 k/2)
-// for even k; 2^(43+c) - 2^(91+c) with c = 39 (k-1)/2 for odd k.
+// for even k; 2^(43+c) - 2^(91+c) = 2^(43+c) (1 - 2^48) with c = 39 (k-1)/2
+// for odd k.  x (1 - 2^48) is an exact signed 64-bit integer (|x| <= 2^15),
+// so the odd case is one sign fix-up and one modular shift.
 template <int K>
 __host__ __device__ __forceinline__ uint64_t i16_mul_w128(int32_t x) {
     if constexpr (K % 2 == 0) {
         return i16_mul_pow2<E_W64 * (K / 2)>(x);
     } else {
         constexpr int c = E_W64 * ((K - 1) / 2);
-        return sub(i16_mul_pow2<43 + c>(x), i16_mul_pow2<91 + c>(x));
+        const uint64_t v = static_cast<uint64_t>(static_cast<int64_t>(x));
+        return mul_pow2<43 + c>(from_i64(v - (v << 48)));
     }
 }
 
