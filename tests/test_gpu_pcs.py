@@ -140,6 +140,17 @@ def test_linearity_ties_combination_to_encode(backend, oracle):
 
 # ---- small primitives ----------------------------------------------------------------
 
+@pytest.mark.parametrize("count", [1, 7, 255, 2049, 70001])
+def test_fp2_powers_counts(backend, oracle, count):
+    """Each thread starts at c^(t+1) and strides by c^T: single-thread, partial
+    and several-stride counts all match the serial powers."""
+    c = (123456789123, int(P - 5))
+    d = backend.fp2_powers_device(c, count)
+    got = backend.download_device(d).view(np.uint64).reshape(-1, 2)
+    backend.free_device(d)
+    assert (got == oracle.fp2_powers(c, count)).all()
+
+
 def test_fp2_powers_and_add(backend, oracle):
     c = (int(P - 2), 123456789)
     d = backend.fp2_powers_device(c, 1000)

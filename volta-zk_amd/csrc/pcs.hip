@@ -56,9 +56,10 @@ int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows
 // - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
 // absorb up to 2^16 rows exactly; the fold to a field element happens once.
 
-constexpr int COMB_COLS = 4;       // columns per thread (one 8-byte i16 load)
+constexpr int COMB_COLS = 8;       // columns per thread (one 16-byte i16 load)
+typedef uint32_t CombWords __attribute__((ext_vector_type(COMB_COLS / 2)));
 constexpr int COMB_THREADS = 256;
-constexpr size_t COMB_CHUNK = 256;  // rows per partial
+constexpr size_t COMB_CHUNK = 128;  // rows per partial
 constexpr int COMB_UNROLL = 8;      // row loads kept in flight per thread
 
 // S[ck][comb][h] = sum over the chunk's rows of component h of coeff[comb][i]
@@ -115,12 +116,13 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
     const bool fast = (j0 + COMB_COLS <= cols) && vec_ok;
     auto load = [&](size_t i, uint32_t* wp) {
         if (fast) {
-            const uint64_t raw = __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(w + i * cols + j0));
-            const uint32_t rx = static_cast<uint32_t>(raw), ry = static_cast<uint32_t>(raw >> 32);
-            wp[0] = (rx & 0xFFFFu) ^ 0x8000u;
-            wp[1] = (rx >> 16) ^ 0x8000u;
-            wp[2] = (ry & 0xFFFFu) ^ 0x8000u;
-            wp[3] = (ry >> 16) ^ 0x8000u;
+            // COMB_COLS i16 in one aligned vector load of COMB_COLS / 2 words
+            const CombWords raw = __builtin_nontemporal_load(reinterpret_cast<const CombWords*>(w + i * cols + j0));
+#pragma unroll
+            for (int q = 0; q < COMB_COLS / 2; ++q) {
+                wp[2 * q] = (raw[q] & 0xFFFFu) ^ 0x8000u;
+                wp[2 * q + 1] = (raw[q] >> 16) ^ 0x8000u;
+            }
         } else {
 #pragma unroll
             for (int q = 0; q < COMB_COLS; ++q) {
@@ -303,8 +305,8 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
     const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
     const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
                     static_cast<unsigned>(chunks));
-    // 8-byte row loads need an 8-byte aligned base and a row pitch of 4k i16.
-    const int vec_ok = (reinterpret_cast<uintptr_t>(w) % 8 == 0) && (cols % 4 == 0);
+    // Vector row loads need a base and a row pitch aligned to COMB_COLS i16.
+    const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * COMB_COLS) == 0) && (cols % COMB_COLS == 0);
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
                 hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
@@ -363,24 +365,36 @@ int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, con
 
 // ---- Fp2 powers [c^1..c^count] (reference fp2_powers_kernel runs serially) ---------------
 
-__global__ void fp2_powers_kernel(Fp2 base, Fp2* out, size_t count) {
+// c^(2^k) for k < 64, computed on the host from the by-value base and passed
+// as a kernel argument (1 KiB of the 4 KiB argument space).
+struct Fp2Squares {
+    Fp2 p[64];
+};
+
+// out[i] = c^(i+1) as the product of c^(2^k) over the set bits of i + 1.  The
+// products go to two accumulators (even and odd k), so the dependent chain is
+// half the bit count; no thread repeats another's squarings.
+__global__ void fp2_powers_kernel(Fp2Squares sq, Fp2* out, size_t count, int bits) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
-        // c^(i+1) by square-and-multiply; each element independent.
-        uint64_t e = i + 1;
-        Fp2 acc{1, 0}, b = base;
-        while (e) {
-            if (e & 1) acc = gl::fp2_mul(acc, b);
-            b = gl::fp2_mul(b, b);
-            e >>= 1;
+        const uint64_t e = i + 1;
+        Fp2 a{1, 0}, b{1, 0};
+        for (int k = 0; k < bits; k += 2) {
+            if ((e >> k) & 1) a = gl::fp2_mul(a, sq.p[k]);
+            if (k + 1 < bits && ((e >> (k + 1)) & 1)) b = gl::fp2_mul(b, sq.p[k + 1]);
         }
-        out[i] = acc;
+        out[i] = gl::fp2_mul(a, b);
     }
 }
 
 int fp2_powers(Context* c, Fp2 base, Fp2* out, size_t count) {
-    hipLaunchKernelGGL(fp2_powers_kernel, dim3(grid_for(count, 256, 8192)), dim3(256), 0, c->stream, base, out,
-                       count);
+    Fp2Squares sq{};
+    int bits = 0;
+    while (bits < 64 && (count >> bits) != 0) ++bits;  // bit length of count >= bit length of i + 1
+    sq.p[0] = base;
+    for (int k = 1; k < bits; ++k) sq.p[k] = gl::fp2_mul(sq.p[k - 1], sq.p[k - 1]);
+    hipLaunchKernelGGL(fp2_powers_kernel, dim3(grid_for(count, 256, 8192)), dim3(256), 0, c->stream, sq, out, count,
+                       bits);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
