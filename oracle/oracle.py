@@ -88,6 +88,12 @@ def _declare(L: ctypes.CDLL) -> None:
         "vo_fnv_u64": (u64, [vp, sz, u64]),
         "vo_fp2_mul_stream": (None, [vp, vp, vp, sz, i32]),
         "vo_fp2_chain": (None, [vp, vp, vp, sz, i32, i32]),
+        "vo_blake3": (None, [vp, sz, vp]),
+        "vo_hash_fp_columns": (None, [vp, sz, sz, vp, i32]),
+        "vo_hash_fp2_columns": (None, [vp, sz, sz, vp, i32]),
+        "vo_merkle_tree": (None, [vp, sz, vp]),
+        "vo_merkle_paths": (None, [vp, sz, vp, sz, vp]),
+        "vo_merkle_bench_matrix": (None, [sz, sz, vp, i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -337,3 +343,58 @@ def fp2_chain(a, b, rounds: int, threads: int | None = None) -> np.ndarray:
     lib().vo_fp2_chain(_ptr(a), _ptr(b), _ptr(out), a.size, rounds,
                        threads or default_threads())
     return fp2_to_u64(out)
+
+
+# ---- BLAKE3 column leaves and Merkle tree (volta_oracle_blake3.c) ------------------------
+
+def blake3(data: bytes) -> bytes:
+    """blake3::hash (blake3 1.8.5, rust/volta-pcs/src/merkle.rs:9-11)."""
+    buf = np.frombuffer(bytes(data), dtype=np.uint8).copy() if data else np.zeros(1, np.uint8)
+    out = np.zeros(32, np.uint8)
+    lib().vo_blake3(_ptr(buf), len(data), _ptr(out))
+    return out.tobytes()
+
+
+def hash_fp_columns(m: np.ndarray, rows: int, cols: int, threads: int | None = None) -> np.ndarray:
+    """cols x 32 bytes: blake3 of each column's LE u64 words (ligero.rs:595-614)."""
+    m = np.ascontiguousarray(m, dtype=np.uint64).reshape(-1)
+    assert m.size == rows * cols
+    out = np.zeros((cols, 32), np.uint8)
+    lib().vo_hash_fp_columns(_ptr(m), rows, cols, _ptr(out), threads or default_threads())
+    return out
+
+
+def hash_fp2_columns(m, rows: int, cols: int, threads: int | None = None) -> np.ndarray:
+    """cols x 32 bytes: blake3 of each column's (c0, c1) LE words."""
+    m = _fp2_array(m).reshape(-1)
+    assert m.size == rows * cols
+    out = np.zeros((cols, 32), np.uint8)
+    lib().vo_hash_fp2_columns(_ptr(m), rows, cols, _ptr(out), threads or default_threads())
+    return out
+
+
+def merkle_tree(leaves: np.ndarray) -> np.ndarray:
+    """(2n - 1) x 32 bytes, levels from the leaves up, root last (merkle.rs:27-37)."""
+    leaves = np.ascontiguousarray(leaves, dtype=np.uint8).reshape(-1, 32)
+    n = leaves.shape[0]
+    assert n >= 1 and n & (n - 1) == 0
+    out = np.zeros((2 * n - 1, 32), np.uint8)
+    lib().vo_merkle_tree(_ptr(leaves), n, _ptr(out))
+    return out
+
+
+def merkle_paths(tree: np.ndarray, leaves: int, indices) -> np.ndarray:
+    """queries x log2(leaves) x 32 bytes of siblings (merkle.rs:43-51)."""
+    tree = np.ascontiguousarray(tree, dtype=np.uint8).reshape(-1, 32)
+    idx = np.ascontiguousarray(indices, dtype=np.uint32)
+    bits = leaves.bit_length() - 1
+    out = np.zeros((idx.size, bits, 32), np.uint8)
+    lib().vo_merkle_paths(_ptr(tree), leaves, _ptr(idx), idx.size, _ptr(out))
+    return out
+
+
+def merkle_bench_matrix(rows: int, cols: int, threads: int | None = None) -> np.ndarray:
+    """M[i] = (i * 0x9E3779B9 + 17) mod p, the reference's Merkle benchmark input."""
+    out = np.zeros(rows * cols, np.uint64)
+    lib().vo_merkle_bench_matrix(rows, cols, _ptr(out), threads or default_threads())
+    return out

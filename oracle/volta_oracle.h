@@ -115,6 +115,17 @@ void vo_fp2_mul_stream(const vo_fp2* a, const vo_fp2* b, vo_fp2* out, size_t n, 
 void vo_fp2_chain(const vo_fp2* a, const vo_fp2* b, vo_fp2* out, size_t n, int rounds,
                   int threads);
 
+/* ---- BLAKE3 column leaves and Merkle tree (volta_oracle_blake3.c) -------
+ * blake3 1.8.5 (rust/Cargo.lock:51-53) restated from the BLAKE3 specification;
+ * merkle.rs:9-51, ligero.rs:595-621. Hashes are 32 bytes. */
+void vo_blake3(const uint8_t* in, size_t len, uint8_t out[32]);               /* blake3::hash */
+void vo_hash_fp_columns(const uint64_t* m, size_t rows, size_t cols, uint8_t* leaves, int threads);
+void vo_hash_fp2_columns(const vo_fp2* m, size_t rows, size_t cols, uint8_t* leaves, int threads);
+void vo_merkle_tree(const uint8_t* leaves, size_t n, uint8_t* tree);         /* merkle.rs:27-37 */
+void vo_merkle_paths(const uint8_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
+                     uint8_t* paths);                                          /* merkle.rs:43-51 */
+void vo_merkle_bench_matrix(size_t rows, size_t cols, uint64_t* m, int threads); /* p7_blake3_merkle.cu:243 */
+
 #ifdef __cplusplus
 }
 #endif

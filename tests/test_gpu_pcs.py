@@ -142,8 +142,8 @@ def test_linearity_ties_combination_to_encode(backend, oracle):
 
 @pytest.mark.parametrize("count", [1, 7, 255, 2049, 70001])
 def test_fp2_powers_counts(backend, oracle, count):
-    """Each thread starts at c^(t+1) and strides by c^T: single-thread, partial
-    and several-stride counts all match the serial powers."""
+    """c^(i+1) as the product of c^(2^k) over the set bits of i+1: a single
+    element, partial blocks and several grid strides match the serial powers."""
     c = (123456789123, int(P - 5))
     d = backend.fp2_powers_device(c, count)
     got = backend.download_device(d).view(np.uint64).reshape(-1, 2)
@@ -247,7 +247,7 @@ def test_geometry_and_id_errors(backend):
     assert "reserved correlation bits" in backend.last_error()
     assert lib.volta_cuda_chacha8_prover_secret_fp_rows_device(raw, out.id, 0, seed, 0, 0, 1) != 0
     # out-of-scope symbols fail explicitly
-    assert lib.volta_cuda_hash_fp_tree_device(raw, out.id, 0, 1, 16, out.id, 0) != 0
+    assert lib.volta_cuda_fp2_mobius_inverse_inplace_device(raw, out.id, 0, 1) != 0
     assert "not implemented" in backend.last_error()
     backend.free_device(again)
     backend.free_device(out)

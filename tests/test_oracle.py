@@ -239,3 +239,66 @@ def test_gather_columns(oracle):
     m = np.arange(24, dtype=np.uint64).reshape(4, 6)
     idx = np.array([5, 0, 3], dtype=np.uint32)
     assert oracle.gather_columns(m, idx).tolist() == [m[:, 5].tolist(), m[:, 0].tolist(), m[:, 3].tolist()]
+
+
+# ---- BLAKE3 column leaves and Merkle tree -------------------------------------------
+
+def test_blake3_published_digests(oracle):
+    for msg, want in spike.BLAKE3_PUBLISHED:
+        assert oracle.blake3(msg).hex() == want
+
+
+def test_merkle16_reference_root(oracle):
+    """rust/volta-pcs/src/merkle.rs:89-96: 1-byte leaves and 64-byte pair hashes."""
+    leaves = np.frombuffer(b"".join(oracle.blake3(bytes([i])) for i in range(16)), np.uint8).reshape(16, 32)
+    assert oracle.merkle_tree(leaves)[-1].tobytes() == spike.MERKLE16_ROOT
+
+
+@pytest.mark.parametrize("rows,cols,want", spike.MERKLE_BENCH_GOLDEN)
+def test_merkle_bench_reference_roots(oracle, rows, cols, want):
+    """One 256-byte chunk per column (32 rows) and 8 chunks per column (1024 rows)."""
+    m = oracle.merkle_bench_matrix(rows, cols)
+    assert (m.reshape(rows, cols) == spike.merkle_bench_matrix(rows, cols)).all()
+    leaves = oracle.hash_fp_columns(m, rows, cols)
+    assert oracle.merkle_tree(leaves)[-1].tobytes().hex() == want
+
+
+def test_column_leaf_bytes_are_le_words_row_by_row(oracle):
+    """A leaf hashes column j's values as LE u64 row by row, an Fp2 as c0 then c1
+    (ligero.rs:351-357): a transposed or word-swapped gather fails."""
+    rnd = np.random.default_rng(5)
+    m = rnd.integers(0, P, size=(9, 4), dtype=np.uint64)
+    leaves = oracle.hash_fp_columns(m, 9, 4)
+    for j in range(4):
+        assert leaves[j].tobytes() == oracle.blake3(b"".join(int(x).to_bytes(8, "little") for x in m[:, j]))
+    m2 = rnd.integers(0, P, size=(5, 2, 2), dtype=np.uint64)
+    leaves2 = oracle.hash_fp2_columns(m2, 5, 2)
+    for j in range(2):
+        data = b"".join(int(m2[i, j, 0]).to_bytes(8, "little") + int(m2[i, j, 1]).to_bytes(8, "little")
+                        for i in range(5))
+        assert leaves2[j].tobytes() == oracle.blake3(data)
+
+
+def _verify_path(oracle, root, idx, leaf, path):
+    """merkle.rs:55-80 restated: fold the siblings from the leaf up."""
+    acc = leaf
+    for sib in path:
+        acc = oracle.blake3(acc + sib) if idx & 1 == 0 else oracle.blake3(sib + acc)
+        idx >>= 1
+    return acc == root
+
+
+def test_merkle_paths_verify_and_detect_tampering(oracle):
+    rnd = np.random.default_rng(9)
+    for n in (2, 8, 64):
+        leaves = rnd.integers(0, 256, size=(n, 32), dtype=np.uint8)
+        tree = oracle.merkle_tree(leaves)
+        root = tree[-1].tobytes()
+        idx = np.arange(n, dtype=np.uint32)
+        paths = oracle.merkle_paths(tree, n, idx)
+        for i in range(n):
+            path = [paths[i, l].tobytes() for l in range(paths.shape[1])]
+            assert _verify_path(oracle, root, i, leaves[i].tobytes(), path)
+            assert not _verify_path(oracle, root, i ^ 1, leaves[i].tobytes(), path)
+        bad = oracle.merkle_paths(tree, n, np.array([n, n + 5], np.uint32))
+        assert not bad.any()  # out-of-range queries read as zero hashes

@@ -548,3 +548,116 @@ VMX_API int volta_mi355x_synchronize(void* raw) {
     if (!c) return -1;
     return sync_stream(c, SyncReason::HostOutput);
 }
+
+// ---------------------------------------------------------------------------
+// BLAKE3 column leaves, Merkle tree and paths
+// ---------------------------------------------------------------------------
+
+namespace {
+
+bool pow2_or_one(size_t n) { return n >= 1 && (n & (n - 1)) == 0; }
+
+// The hash kernels move 32-byte hashes with 16-byte vector accesses.
+int hash_aligned(Context* c, const void* p, const char* what) {
+    if (reinterpret_cast<uintptr_t>(p) % 16 != 0) {
+        std::string m = std::string(what) + " region must be 16-byte aligned";
+        return fail_msg(c, m.c_str());
+    }
+    return 0;
+}
+
+int hash_tree_device(Context* c, uint64_t m_id, size_t m_off, size_t rows, size_t cols, uint64_t tree_id,
+                     size_t tree_off_bytes, bool fp2) {
+    size_t mn = 0, tb = 0;
+    if (!mul_ok(rows, cols, &mn) || !mul_ok(2 * cols - 1, 32, &tb))
+        return fail_msg(c, "resident Merkle geometry overflows size_t");
+    void *m = nullptr, *tree = nullptr;
+    if (region_elems(c, m_id, m_off, mn, fp2 ? 16 : 8, &m) || region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree))
+        return -1;
+    if (hash_aligned(c, tree, "Merkle tree")) return -1;
+    if (begin_op(c) || mark_op(c, 1)) return -1;
+    uint32_t* t = static_cast<uint32_t*>(tree);
+    if (merkle_column_leaves(c, static_cast<const uint64_t*>(m), rows, cols, fp2, t) ||
+        merkle_tree_levels(c, t, cols))
+        return -1;
+    if (mark_op(c, 2)) return -1;
+    return finish_op(c, OP_PCS_MERKLE, 0, 0);
+}
+
+}  // namespace
+
+// Replaces volta_cuda_hash_fp_tree_device (.cu:7166-7175, hash_tree_device_impl
+// .cu:7151-7164): leaves = blake3 of each column of the rows x cols Fp matrix,
+// then the Merkle levels; (2 cols - 1) hashes at the tree's byte offset.
+VMX_API int volta_cuda_hash_fp_tree_device(void* raw, uint64_t matrix_id, size_t matrix_off, size_t rows, size_t cols,
+                                              uint64_t tree_id, size_t tree_off_bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2_or_one(cols)) return fail_msg(c, "invalid resident Fp Merkle geometry");
+    return guarded(c, "resident Fp Merkle tree",
+                   [&] { return hash_tree_device(c, matrix_id, matrix_off, rows, cols, tree_id, tree_off_bytes, false); });
+}
+
+// Replaces volta_cuda_hash_fp2_tree_device (.cu:7177-7186): the same over an
+// Fp2 matrix, each element hashed as c0 then c1.
+VMX_API int volta_cuda_hash_fp2_tree_device(void* raw, uint64_t matrix_id, size_t matrix_off, size_t rows,
+                                               size_t cols, uint64_t tree_id, size_t tree_off_bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !pow2_or_one(cols)) return fail_msg(c, "invalid resident Fp2 Merkle geometry");
+    return guarded(c, "resident Fp2 Merkle tree",
+                   [&] { return hash_tree_device(c, matrix_id, matrix_off, rows, cols, tree_id, tree_off_bytes, true); });
+}
+
+// Replaces volta_cuda_merkle_paths_device (.cu:7188-7204): for each query the
+// log2(leaves) sibling hashes from the leaf level up (MerkleTree::open,
+// rust/volta-pcs/src/merkle.rs:43-51).  Indices are validated by the Rust seam
+// (rust/volta-accel/src/lib.rs:6735-6760); an out-of-range index yields zero
+// hashes instead of reading outside the tree.
+VMX_API int volta_cuda_merkle_paths_device(void* raw, uint64_t tree_id, size_t tree_off_bytes, size_t leaves,
+                                              uint64_t idx_id, size_t idx_off, size_t queries, uint64_t paths_id,
+                                              size_t paths_off_bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !pow2(leaves) || !queries) return fail_msg(c, "invalid resident Merkle path geometry");
+    return guarded(c, "resident Merkle paths", [&] {
+        size_t bits = 0;
+        while ((size_t{1} << bits) < leaves) ++bits;
+        size_t tb = 0, pb = 0;
+        if (!mul_ok(2 * leaves - 1, 32, &tb) || !mul_ok(queries * bits, 32, &pb))
+            return fail_msg(c, "resident Merkle path geometry overflows size_t");
+        void *tree = nullptr, *idx = nullptr, *paths = nullptr;
+        if (region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree) ||
+            region_elems(c, idx_id, idx_off, queries, 4, &idx) ||
+            region_elems(c, paths_id, paths_off_bytes, pb, 1, &paths))
+            return -1;
+        if (hash_aligned(c, tree, "Merkle tree") || hash_aligned(c, paths, "Merkle path")) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (merkle_paths(c, static_cast<const uint32_t*>(tree), leaves, static_cast<const uint32_t*>(idx), queries,
+                         static_cast<uint32_t*>(paths)))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_MERKLE, 0, 0);
+    });
+}
+
+// Replaces volta_cuda_hash_fp_columns (.cu:7256-7265; caller
+// Backend::hash_fp_columns, rust/volta-accel/src/lib.rs:6380-6405): host
+// rows x cols Fp matrix in, cols x 32 leaf bytes out.  Same geometry rule:
+// rows >= 8, rows % 8 == 0, cols a power of two.
+VMX_API int volta_cuda_hash_fp_columns(void* raw, const uint64_t* matrix, size_t rows, size_t cols, uint8_t* leaves) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !matrix || !leaves || rows < 8 || rows % 8 || !pow2_or_one(cols))
+        return fail_msg(c, "invalid PCS hash matrix geometry");
+    return guarded(c, "PCS column hashes", [&] {
+        size_t mb = 0;
+        if (!mul_ok(rows * cols, 8, &mb) || rows * cols / cols != rows)
+            return fail_msg(c, "PCS hash matrix geometry overflows size_t");
+        const size_t hb = cols * 32;
+        if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_OUT, hb)) return -1;
+        if (begin_op(c)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
+        if (mark_op(c, 1)) return -1;
+        if (merkle_column_leaves(c, ws<uint64_t>(c, WS_IN), rows, cols, false, ws<uint32_t>(c, WS_OUT))) return -1;
+        if (mark_op(c, 2)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(leaves, ws<void>(c, WS_OUT), hb, hipMemcpyDeviceToHost, c->stream));
+        return finish_op(c, OP_PCS_MERKLE, mb, hb);
+    });
+}

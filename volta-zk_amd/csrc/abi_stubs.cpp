@@ -324,10 +324,6 @@ VMX_API int volta_cuda_logup_aux_round_into_device(void* ctx, uint64_t a1, size_
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8, (void)a9, (void)a10, (void)a11, (void)a12, (void)a13, (void)a14, (void)a15, (void)a16, (void)a17, (void)a18, (void)a19, (void)a20, (void)a21, (void)a22; return vmx_out_of_scope(ctx, "volta_cuda_logup_aux_round_into_device");
 }
 
-VMX_API int volta_cuda_hash_fp_columns(void* ctx, const uint64_t* a1, size_t a2, size_t a3, uint8_t* a4) {
-    (void)a1, (void)a2, (void)a3, (void)a4; return vmx_out_of_scope(ctx, "volta_cuda_hash_fp_columns");
-}
-
 VMX_API int volta_cuda_fp2_mobius_inverse_inplace_device(void* ctx, uint64_t a1, size_t a2, size_t a3) {
     (void)a1, (void)a2, (void)a3; return vmx_out_of_scope(ctx, "volta_cuda_fp2_mobius_inverse_inplace_device");
 }
@@ -336,14 +332,3 @@ VMX_API int volta_cuda_fp2_affine_eq_weights_inplace_device(void* ctx, uint64_t 
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8, (void)a9, (void)a10; return vmx_out_of_scope(ctx, "volta_cuda_fp2_affine_eq_weights_inplace_device");
 }
 
-VMX_API int volta_cuda_hash_fp_tree_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_hash_fp_tree_device");
-}
-
-VMX_API int volta_cuda_hash_fp2_tree_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_hash_fp2_tree_device");
-}
-
-VMX_API int volta_cuda_merkle_paths_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, size_t a8) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8; return vmx_out_of_scope(ctx, "volta_cuda_merkle_paths_device");
-}

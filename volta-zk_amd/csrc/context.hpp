@@ -167,6 +167,7 @@ enum WorkspaceSlot : int {
     WS_PARTIALS = 4,  // combination partial sums
     WS_TRANSPOSE = 5, // four-step intermediate
     WS_AUX2 = 6,      // combination coefficient sums
+    WS_HASH = 7,      // Merkle column-group chaining values
     WS_COUNT = 8,
 };
 

@@ -46,6 +46,14 @@ int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, si
 int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows,
                             size_t count, size_t padded, gl::Fp2* out);
 
+// BLAKE3 column leaves of a rows x cols Fp (fp2 = false) or Fp2 matrix into
+// leaves[cols][8 words]; the Merkle levels above cols leaves stored after
+// them (tree = leaves, then each level, root last); sibling paths.
+int merkle_column_leaves(Context* c, const uint64_t* m, size_t rows, size_t cols, bool fp2, uint32_t* leaves);
+int merkle_tree_levels(Context* c, uint32_t* tree, size_t leaves);
+int merkle_paths(Context* c, const uint32_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
+                 uint32_t* paths);
+
 // Measurement probes.
 int probe_copy(Context* c, const void* src, void* dst, size_t bytes);
 int probe_fp2_stream(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n);

@@ -187,6 +187,14 @@ class DeviceBuffer:
         return self.len * self.dtype.itemsize
 
 
+@dataclass
+class DeviceMerkleTree:
+    """A resident BLAKE3 column tree (rust DeviceMerkleTree, lib.rs:6700-6725):
+    storage holds (2 leaves - 1) 32-byte hashes, leaves first, root last."""
+    storage: DeviceBuffer
+    leaves: int
+
+
 def _as_fp2(a) -> np.ndarray:
     a = np.ascontiguousarray(a)
     if a.dtype == FP2:
@@ -535,6 +543,52 @@ class Backend:
         return out
 
     # ---- helpers ---------------------------------------------------------------------------
+    # ---- BLAKE3 column leaves and Merkle tree (lib.rs:6380-6405, 6677-6770) ------------
+    def _hash_tree_device(self, matrix: DeviceBuffer, rows: int, cols: int, fp2: bool) -> DeviceMerkleTree:
+        if rows == 0 or cols == 0 or cols & (cols - 1):
+            raise InvalidInput("invalid resident Merkle matrix geometry")
+        self._region(matrix, 0, rows * cols)
+        storage = self.alloc_device((2 * cols - 1) * 32, np.uint8)
+        fn = self.lib.volta_cuda_hash_fp2_tree_device if fp2 else self.lib.volta_cuda_hash_fp_tree_device
+        self._call_or_free(storage, fn, matrix.id, 0, rows, cols, storage.id, 0)
+        return DeviceMerkleTree(storage, cols)
+
+    def hash_fp_tree_device(self, matrix: DeviceBuffer, rows: int, cols: int) -> DeviceMerkleTree:
+        """Leaves = blake3 of each column of the rows x cols Fp matrix, then the tree."""
+        return self._hash_tree_device(matrix, rows, cols, False)
+
+    def hash_fp2_tree_device(self, matrix: DeviceBuffer, rows: int, cols: int) -> DeviceMerkleTree:
+        """The same over an Fp2 matrix, each element hashed as c0 then c1."""
+        return self._hash_tree_device(matrix, rows, cols, True)
+
+    def merkle_root_device(self, tree: DeviceMerkleTree) -> bytes:
+        self._own(tree.storage)
+        return self.download_device(tree.storage, (2 * tree.leaves - 2) * 32, 32).tobytes()
+
+    def merkle_paths_device(self, tree: DeviceMerkleTree, indices: DeviceBuffer, queries: int) -> DeviceBuffer:
+        """queries x log2(leaves) sibling hashes (32 bytes each), leaf level first."""
+        self._own(tree.storage)
+        self._region(indices, 0, queries)
+        if queries == 0:
+            raise InvalidInput("empty resident Merkle query set")
+        bits = tree.leaves.bit_length() - 1
+        paths = self.alloc_device(max(queries * bits * 32, 1), np.uint8)
+        self._call_or_free(paths, self.lib.volta_cuda_merkle_paths_device, tree.storage.id, 0, tree.leaves,
+                           indices.id, 0, queries, paths.id, 0)
+        return paths
+
+    def free_device_merkle_tree(self, tree: DeviceMerkleTree) -> None:
+        self.free_device(tree.storage)
+
+    def hash_fp_columns(self, matrix: np.ndarray, rows: int, cols: int) -> np.ndarray:
+        """Host form: cols x 32 leaf bytes (lib.rs:6380-6405, same geometry rule)."""
+        m = np.ascontiguousarray(matrix, dtype=np.uint64).reshape(-1)
+        if rows < 8 or rows % 8 or cols == 0 or cols & (cols - 1) or m.size != rows * cols:
+            raise InvalidInput("invalid PCS hash matrix geometry")
+        out = np.empty((cols, 32), np.uint8)
+        self._check(self.lib.volta_cuda_hash_fp_columns(self.raw, m.ctypes.data, rows, cols, out.ctypes.data))
+        return out
+
     def _call_or_free(self, out: DeviceBuffer, fn, *args) -> None:
         rc = fn(self.raw, *args)
         if rc != 0:
