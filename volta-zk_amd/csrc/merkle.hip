@@ -9,21 +9,23 @@
 //
 // BLAKE3 cuts a column's byte stream into 1024-byte chunks (128 Fp rows or 64
 // Fp2 rows) and joins chunk chaining values in a binary tree whose left
-// subtrees are complete power-of-two blocks.  On the GPU:
-//   column_groups: one thread per (column, aligned group of G chunks).  A
-//     wave's lanes are 64 consecutive columns, so every row read is one
-//     coalesced 512-byte (Fp) or 1 KiB (Fp2) segment.  The thread hashes its
-//     chunks in order, prefetching the next block's 8 words while it
-//     compresses the current one, and merges chunk values eagerly on a small
-//     per-lane stack in LDS.  Aligned groups of a power-of-two size are exact
-//     subtrees of the BLAKE3 tree, and a short last group is the subtree over
-//     the remaining chunks.
-//   merge_groups: one workgroup per column joins its group values level by
-//     level, carrying an odd last node up unchanged; that pairing builds the
-//     same left-complete tree, and the last join carries the ROOT flag.
+// subtrees are complete power-of-two blocks.  Any aligned power-of-two run of
+// chunks is therefore an exact subtree, and a short run at the end is the
+// left-complete subtree over what remains; the GPU builds the tree in such
+// runs, bottom up:
+//   column_groups: one thread per (column, run of up to 4 chunks).  A wave's
+//     lanes are 64 consecutive columns, so every row read is one coalesced
+//     512-byte (Fp) or 1 KiB (Fp2) segment.  The thread hashes its chunks in
+//     order, loading the next block while it compresses the current one, and
+//     joins them with two registers of pending values (no LDS, so occupancy
+//     is set by registers alone).
+//   merge_pass: one thread per (column, run of 16 values) folds them with an
+//     eager join stack in LDS, repeated until one value per column is left;
+//     the column's last join carries the ROOT flag.
 //   merkle_level / merkle_top: the pair hashes of the Merkle tree.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <array>
 
 #include "context.hpp"
@@ -63,41 +65,78 @@ __device__ __forceinline__ void g(uint32_t& a, uint32_t& b, uint32_t& c, uint32_
     b = rotr(b ^ c, 7);
 }
 
-// cv <- the chaining value of compress(cv, m, counter, block_len, flags).
-__device__ __forceinline__ void compress(uint32_t* cv, const uint32_t* m, uint64_t counter, uint32_t block_len,
-                                         uint32_t flags) {
-    uint32_t v[16] = {cv[0],  cv[1],  cv[2],  cv[3],  cv[4],  cv[5],
-                      cv[6],  cv[7],  IV[0],  IV[1],  IV[2],  IV[3],
-                      static_cast<uint32_t>(counter), static_cast<uint32_t>(counter >> 32), block_len, flags};
+// cv[s] <- the chaining value of compress(cv[s], m[s], counter, block_len,
+// flags) for S independent states, their G functions interleaved so one
+// lane keeps several dependency chains in flight.
+template <int S>
+__device__ __forceinline__ void compress_n(uint32_t (*cv)[8], const uint32_t (*m)[16], uint64_t counter,
+                                           uint32_t block_len, uint32_t flags) {
+    uint32_t v[S][16];
+#pragma unroll
+    for (int q = 0; q < S; ++q) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[q][i] = cv[q][i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[q][8 + i] = IV[i];
+        v[q][12] = static_cast<uint32_t>(counter);
+        v[q][13] = static_cast<uint32_t>(counter >> 32);
+        v[q][14] = block_len;
+        v[q][15] = flags;
+    }
     gl::static_for<0, 7>([&](auto rr) {
         constexpr auto s = SCHED[decltype(rr)::value];
-        g(v[0], v[4], v[8], v[12], m[s[0]], m[s[1]]);
-        g(v[1], v[5], v[9], v[13], m[s[2]], m[s[3]]);
-        g(v[2], v[6], v[10], v[14], m[s[4]], m[s[5]]);
-        g(v[3], v[7], v[11], v[15], m[s[6]], m[s[7]]);
-        g(v[0], v[5], v[10], v[15], m[s[8]], m[s[9]]);
-        g(v[1], v[6], v[11], v[12], m[s[10]], m[s[11]]);
-        g(v[2], v[7], v[8], v[13], m[s[12]], m[s[13]]);
-        g(v[3], v[4], v[9], v[14], m[s[14]], m[s[15]]);
+#pragma unroll
+        for (int q = 0; q < S; ++q) {
+            g(v[q][0], v[q][4], v[q][8], v[q][12], m[q][s[0]], m[q][s[1]]);
+            g(v[q][1], v[q][5], v[q][9], v[q][13], m[q][s[2]], m[q][s[3]]);
+            g(v[q][2], v[q][6], v[q][10], v[q][14], m[q][s[4]], m[q][s[5]]);
+            g(v[q][3], v[q][7], v[q][11], v[q][15], m[q][s[6]], m[q][s[7]]);
+        }
+#pragma unroll
+        for (int q = 0; q < S; ++q) {
+            g(v[q][0], v[q][5], v[q][10], v[q][15], m[q][s[8]], m[q][s[9]]);
+            g(v[q][1], v[q][6], v[q][11], v[q][12], m[q][s[10]], m[q][s[11]]);
+            g(v[q][2], v[q][7], v[q][8], v[q][13], m[q][s[12]], m[q][s[13]]);
+            g(v[q][3], v[q][4], v[q][9], v[q][14], m[q][s[14]], m[q][s[15]]);
+        }
     });
 #pragma unroll
-    for (int i = 0; i < 8; ++i) cv[i] = v[i] ^ v[i + 8];
+    for (int q = 0; q < S; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cv[q][i] = v[q][i] ^ v[q][i + 8];
 }
 
-// out <- compress(IV, l || r, 0, 64, flags): a BLAKE3 parent node (flags
-// PARENT [| ROOT]) or, with CHUNK_START | CHUNK_END | ROOT, the hash of the
-// 64 bytes l || r as a message (the Merkle pair hash).
+__device__ __forceinline__ void compress(uint32_t* cv, const uint32_t* m, uint64_t counter, uint32_t block_len,
+                                         uint32_t flags) {
+    compress_n<1>(reinterpret_cast<uint32_t(*)[8]>(cv), reinterpret_cast<const uint32_t(*)[16]>(m), counter,
+                  block_len, flags);
+}
+
+// out[s] <- compress(IV, l[s] || r[s], 0, 64, flags) for S pairs: BLAKE3
+// parent nodes (flags PARENT [| ROOT]) or, with CHUNK_START | CHUNK_END |
+// ROOT, the hash of the 64 bytes l || r as a message (the Merkle pair hash).
+template <int S>
+__device__ __forceinline__ void join_n(uint32_t (*out)[8], const uint32_t (*l)[8], const uint32_t (*r)[8],
+                                       uint32_t flags) {
+    uint32_t m[S][16], cv[S][8];
+#pragma unroll
+    for (int q = 0; q < S; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            m[q][i] = l[q][i];
+            m[q][8 + i] = r[q][i];
+            cv[q][i] = IV[i];
+        }
+    compress_n<S>(cv, m, 0, 64, flags);
+#pragma unroll
+    for (int q = 0; q < S; ++q)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[q][i] = cv[q][i];
+}
+
 __device__ __forceinline__ void join(uint32_t* out, const uint32_t* l, const uint32_t* r, uint32_t flags) {
-    uint32_t m[16], cv[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        m[i] = l[i];
-        m[8 + i] = r[i];
-        cv[i] = IV[i];
-    }
-    compress(cv, m, 0, 64, flags);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) out[i] = cv[i];
+    join_n<1>(reinterpret_cast<uint32_t(*)[8]>(out), reinterpret_cast<const uint32_t(*)[8]>(l),
+              reinterpret_cast<const uint32_t(*)[8]>(r), flags);
 }
 
 __device__ __forceinline__ void store_hash(uint32_t* dst, const uint32_t* h) {
@@ -114,97 +153,152 @@ __device__ __forceinline__ void load_hash(uint32_t* h, const uint32_t* src) {
 
 constexpr int LANES = 64;          // columns per column_groups workgroup (one wave)
 constexpr size_t CHUNK_WORDS = 128; // u64 words per 1024-byte chunk
-constexpr size_t MAX_GROUPS = 256;  // merge_groups handles up to this many groups per column
-constexpr size_t MAX_GROUP = 4096;  // chunks per group (LDS stack depth 13)
 
-// W = u64 words per matrix element: 1 for Fp, 2 for Fp2.  Writes the group's
-// chaining value to out[(g cols + col) 8 ..], or with root set (one group
-// per column) the column's leaf hash to out[col 8 ..].
-template <int W>
+// W = u64 words per matrix element: 1 for Fp, 2 for Fp2.  Thread (column,
+// g) hashes the chunks [g G, min(g G + G, chunks)) of its column, G <= 4, and
+// joins them left-complete with two registers of pending values: chunks 0+1
+// and 2+3 pair up, then the pairs; a short last group of 3 joins (0+1)+2.
+// Writes the group's chaining value to out[(g cols + col) 8 ..], or with
+// root set (one group per column) the column's leaf hash to out[col 8 ..].
+// OFF32: a row of the matrix spans less than 4 GiB, so a lane's element is
+// addressed as the uniform row pointer plus a 32-bit byte offset.
+template <int W, bool OFF32>
 __global__ __launch_bounds__(LANES) void column_groups(const uint64_t* __restrict__ m, size_t rows, size_t cols,
                                                        size_t chunks, size_t group, int root,
                                                        uint32_t* __restrict__ out) {
-    extern __shared__ uint32_t stack[];  // [depth][8 words][LANES]
     const int lane = threadIdx.x;
     const size_t col = static_cast<size_t>(blockIdx.x) * LANES + lane;
-    if (col >= cols) return;  // no barriers below: the stack is per lane
+    if (col >= cols) return;
     const size_t gi = blockIdx.y;
     const size_t c_begin = gi * group;
     const size_t c_end = min(chunks, c_begin + group);
-    const size_t words = rows * W;  // the column's u64 word stream
+    const size_t n_local = c_end - c_begin;  // 1..4
+    const size_t words = rows * W;            // the column's u64 word stream
     const size_t row_stride = cols * W;
-    const uint64_t* base = m + col * W;
+    const uint32_t lane_bytes = static_cast<uint32_t>(col * W * sizeof(uint64_t));  // used when OFF32
+    // blocks of the group in stream order: only the column's last chunk can
+    // be short, and it comes last, so block k starts at word (c_begin 16 + k) 8
+    const size_t last_words = words - (c_end - 1) * CHUNK_WORDS;
+    const size_t total = (n_local - 1) * 16 + (min(CHUNK_WORDS, last_words) + 7) / 8;
 
-    auto blocks_in = [&](size_t c) -> int {
-        const size_t w = min(CHUNK_WORDS, words - c * CHUNK_WORDS);
-        return static_cast<int>((w + 7) / 8);
+    auto element = [&](size_t row, int part) -> const uint64_t* {
+        const uint64_t* rowp = m + row * row_stride;
+        if constexpr (OFF32)
+            return reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(rowp) + lane_bytes) + part;
+        else
+            return rowp + col * W + part;
     };
-    // block b of chunk c: stream words [c 128 + 8 b, + 8), zero past the end
-    auto load_block = [&](size_t c, int b, uint32_t* mw) {
-        const size_t w0 = c * CHUNK_WORDS + static_cast<size_t>(b) * 8;
+    auto load_block = [&](size_t k, uint32_t* mw) {
+        const size_t w0 = (c_begin * 16 + k) * 8;
+        if (w0 + 8 <= words) {
+            if constexpr (W == 1) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const size_t w = w0 + k;
-            const size_t row = w / W, part = w - row * W;
-            const uint64_t x = w < words ? base[row * row_stride + part] : 0;
-            mw[2 * k] = static_cast<uint32_t>(x);
-            mw[2 * k + 1] = static_cast<uint32_t>(x >> 32);
+                for (int i = 0; i < 8; ++i) {
+                    const uint64_t x = *element(w0 + i, 0);
+                    mw[2 * i] = static_cast<uint32_t>(x);
+                    mw[2 * i + 1] = static_cast<uint32_t>(x >> 32);
+                }
+            } else {
+                using u32x4 = uint32_t __attribute__((ext_vector_type(4)));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {  // one 16-byte (c0, c1) load per row
+                    const u32x4 x = *reinterpret_cast<const u32x4*>(element(w0 / 2 + i, 0));
+                    mw[4 * i] = x.x, mw[4 * i + 1] = x.y, mw[4 * i + 2] = x.z, mw[4 * i + 3] = x.w;
+                }
+            }
+        } else {  // the column's last, partial block: zero past the end
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const size_t w = w0 + i;
+                const uint64_t x = w < words ? *element(w / W, static_cast<int>(w % W)) : 0;
+                mw[2 * i] = static_cast<uint32_t>(x);
+                mw[2 * i + 1] = static_cast<uint32_t>(x >> 32);
+            }
         }
     };
-    auto push = [&](int d, const uint32_t* h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) stack[(d * 8 + i) * LANES + lane] = h[i];
-    };
-    auto peek = [&](int d, uint32_t* h) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = stack[(d * 8 + i) * LANES + lane];
-    };
 
-    int depth = 0;
-    uint32_t cv[8], nxt[16];
-    size_t c = c_begin;
-    int b = 0, blocks = blocks_in(c);
-    load_block(c, 0, nxt);
-    while (c < c_end) {
-        uint32_t cur[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) cur[i] = nxt[i];
-        const size_t cc = c;
-        const int cb = b, cblocks = blocks;
-        if (++b == blocks) {
-            ++c;
-            b = 0;
-            if (c < c_end) blocks = blocks_in(c);
-        }
-        if (c < c_end) load_block(c, b, nxt);  // in flight during the compression below
-
-        const size_t left = words - cc * CHUNK_WORDS - static_cast<size_t>(cb) * 8;
+    const uint32_t top = root ? PARENT | ROOT : PARENT;  // flags of the group's last join
+    uint32_t cv[8], p0[8], p1[8];
+    // compress block k; at a chunk's end fold the chunk into p0 / p1
+    auto step = [&](const uint32_t* mw, size_t k) {
+        const int lc = static_cast<int>(k / 16);  // chunk within the group
+        const int cb = static_cast<int>(k % 16);
+        const bool chunk_end = (cb == 15) || (k + 1 == total);
+        const size_t left = words - (c_begin * 16 + k) * 8;
         const uint32_t len = static_cast<uint32_t>(min<size_t>(8, left) * 8);
         if (cb == 0)
 #pragma unroll
             for (int i = 0; i < 8; ++i) cv[i] = IV[i];
-        uint32_t flags = (cb == 0 ? CHUNK_START : 0u) | (cb + 1 == cblocks ? CHUNK_END : 0u);
-        if (chunks == 1 && cb + 1 == cblocks) flags |= ROOT;  // a one-chunk column: this block is the root
-        compress(cv, cur, cc, len, flags);
-        if (cb + 1 != cblocks) continue;
-        if (chunks == 1) {
-            store_hash(out + col * 8, cv);
-            return;
+        uint32_t flags = (cb == 0 ? CHUNK_START : 0u) | (chunk_end ? CHUNK_END : 0u);
+        if (chunks == 1 && chunk_end) flags |= ROOT;  // a one-chunk column: this block is the root
+        compress(cv, mw, c_begin + lc, len, flags);
+        if (!chunk_end) return;
+        if (lc == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p0[i] = cv[i];
+        } else if (lc == 1) {
+            join(p0, p0, cv, n_local == 2 ? top : PARENT);
+        } else if (lc == 2) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) p1[i] = cv[i];
+        } else {
+            join(p1, p1, cv, PARENT);
+            join(p0, p0, p1, top);
         }
-        push(depth++, cv);
-        size_t t = cc - c_begin + 1;  // chunks of this group done
-        if (t < c_end - c_begin) {
-            // eager joins of complete power-of-two runs; the group's last
-            // chunk is joined in the final fold so the root join can be flagged
-            while ((t & 1) == 0) {
-                uint32_t l[8], r[8], p[8];
-                peek(depth - 1, r);
-                peek(depth - 2, l);
-                join(p, l, r, PARENT);
-                depth -= 2;
-                push(depth++, p);
-                t >>= 1;
-            }
+    };
+
+    // two buffers: the next block loads while the current one compresses
+    uint32_t a[16], b[16];
+    load_block(0, a);
+    for (size_t k = 0;;) {
+        if (k + 1 < total) load_block(k + 1, b);
+        step(a, k);
+        if (++k == total) break;
+        if (k + 1 < total) load_block(k + 1, a);
+        step(b, k);
+        if (++k == total) break;
+    }
+    if (n_local == 3) join(p0, p0, p1, top);
+    store_hash(out + (root ? col : gi * cols + col) * 8, p0);
+}
+
+constexpr int FAN_IN = 16;      // values one merge_pass thread folds
+constexpr int MERGE_DEPTH = 5;  // pending values of a left-complete fold of 16
+
+// Thread (column, j) folds values [16 j, min(16 j + 16, k_in)) of its column
+// (in[(i cols + col) 8 ..]) left-complete, joining complete power-of-two runs
+// eagerly on a per-lane LDS stack; with final set this is the column's last
+// fold and its top join carries ROOT.  k_in >= 2.
+__global__ __launch_bounds__(LANES) void merge_pass(const uint32_t* __restrict__ in, size_t k_in, size_t cols,
+                                                    int final, uint32_t* __restrict__ out) {
+    __shared__ uint32_t stack[MERGE_DEPTH][8][LANES];
+    const int lane = threadIdx.x;
+    const size_t col = static_cast<size_t>(blockIdx.x) * LANES + lane;
+    if (col >= cols) return;
+    const size_t j = blockIdx.y;
+    const size_t i0 = j * FAN_IN;
+    const size_t n = min<size_t>(FAN_IN, k_in - i0);
+    auto push = [&](int d, const uint32_t* h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) stack[d][i][lane] = h[i];
+    };
+    auto peek = [&](int d, uint32_t* h) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[i] = stack[d][i][lane];
+    };
+    int depth = 0;
+    for (size_t t = 1; t <= n; ++t) {
+        uint32_t h[8];
+        load_hash(h, in + ((i0 + t - 1) * cols + col) * 8);
+        push(depth++, h);
+        if (t == n) break;  // the last value is joined in the fold below
+        for (size_t u = t; (u & 1) == 0; u >>= 1) {
+            uint32_t l[8], r[8], p[8];
+            peek(depth - 1, r);
+            peek(depth - 2, l);
+            join(p, l, r, PARENT);
+            depth -= 2;
+            push(depth++, p);
         }
     }
     uint32_t acc[8];
@@ -212,54 +306,9 @@ __global__ __launch_bounds__(LANES) void column_groups(const uint64_t* __restric
     while (depth > 0) {
         uint32_t l[8];
         peek(--depth, l);
-        join(acc, l, acc, PARENT | (depth == 0 && root ? ROOT : 0u));
+        join(acc, l, acc, PARENT | (depth == 0 && final ? ROOT : 0u));
     }
-    store_hash(out + (root ? col : gi * cols + col) * 8, acc);
-}
-
-// One workgroup per column: joins the column's `groups` chaining values
-// (gcv[(g cols + col) 8 ..]) level by level into the leaf hash.
-__global__ __launch_bounds__(MAX_GROUPS) void merge_groups(const uint32_t* __restrict__ gcv, size_t groups,
-                                                           size_t cols, uint32_t* __restrict__ leaves) {
-    __shared__ uint32_t node[MAX_GROUPS][9];  // odd pitch: a join reads two nodes per lane
-    const size_t col = blockIdx.x;
-    const int t = threadIdx.x;
-    if (static_cast<size_t>(t) < groups) {
-        uint32_t h[8];
-        load_hash(h, gcv + (t * cols + col) * 8);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) node[t][i] = h[i];
-    }
-    __syncthreads();
-    int count = static_cast<int>(groups);
-    while (count > 1) {
-        const int pairs = count / 2;
-        uint32_t p[8];
-        if (t < pairs) {
-            uint32_t l[8], r[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                l[i] = node[2 * t][i];
-                r[i] = node[2 * t + 1][i];
-            }
-            join(p, l, r, PARENT | (count == 2 ? ROOT : 0u));
-        }
-        __syncthreads();
-        if (t < pairs)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) node[t][i] = p[i];
-        if ((count & 1) && t == pairs)  // carry the odd last node up unchanged
-#pragma unroll
-            for (int i = 0; i < 8; ++i) node[pairs][i] = node[count - 1][i];
-        __syncthreads();
-        count = pairs + (count & 1);
-    }
-    if (t == 0) {
-        uint32_t h[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) h[i] = node[0][i];
-        store_hash(leaves + col * 8, h);
-    }
+    store_hash(out + (final ? col : j * cols + col) * 8, acc);
 }
 
 constexpr uint32_t PAIR_FLAGS = CHUNK_START | CHUNK_END | ROOT;  // blake3 of a 64-byte message
@@ -340,50 +389,47 @@ __global__ __launch_bounds__(256) void merkle_paths_kernel(const uint32_t* __res
 
 }  // namespace b3
 
-namespace {
-
-size_t log2_exact(size_t n) {
-    size_t b = 0;
-    while ((size_t{1} << b) < n) ++b;
-    return b;
-}
-
-}  // namespace
 
 int merkle_column_leaves(Context* c, const uint64_t* m, size_t rows, size_t cols, bool fp2, uint32_t* leaves) {
     const size_t w = fp2 ? 2 : 1;
     const size_t words = rows * w;
     const size_t chunks = (words + b3::CHUNK_WORDS - 1) / b3::CHUNK_WORDS;
-    // Groups: enough threads to fill the GPU (about 16 waves per CU), at most
-    // MAX_GROUPS per column for merge_groups.
-    constexpr size_t TARGET_THREADS = size_t{1} << 18;
-    size_t group = 1;
-    while (group < chunks && cols * ((chunks + 2 * group - 1) / (2 * group)) >= TARGET_THREADS) group *= 2;
-    while ((chunks + group - 1) / group > b3::MAX_GROUPS) group *= 2;
-    if (group > b3::MAX_GROUP) return fail_msg(c, "Merkle column too long (more than 2^20 BLAKE3 chunks)");
-    const size_t groups = (chunks + group - 1) / group;
-    const int depth = static_cast<int>(log2_exact(group)) + 1;
-    const size_t lds = static_cast<size_t>(depth) * 8 * b3::LANES * sizeof(uint32_t);
-    uint32_t* gout = leaves;
-    if (groups > 1) {
+    const size_t group = std::min<size_t>(4, chunks);  // chunks per column_groups thread
+    size_t k = (chunks + group - 1) / group;           // values per column after column_groups
+    if (k > 65535) return fail_msg(c, "Merkle column too long (more than 2^18 BLAKE3 chunks)");
+    // workspace: column_groups' values, then each non-final merge pass's (16x fewer)
+    size_t slots = 0;
+    for (size_t kk = k; kk > 1; kk = (kk + b3::FAN_IN - 1) / b3::FAN_IN) slots += kk;
+    uint32_t* buf = nullptr;
+    if (k > 1) {
         size_t bytes = 0;
-        if (!mul_ok(groups * cols, 32, &bytes)) return fail_msg(c, "Merkle group buffer overflows size_t");
+        if (!mul_ok(slots, cols * 32, &bytes)) return fail_msg(c, "Merkle workspace overflows size_t");
         if (ensure_ws(c, WS_HASH, bytes)) return -1;
-        gout = ws<uint32_t>(c, WS_HASH);
+        buf = ws<uint32_t>(c, WS_HASH);
     }
-    const dim3 grid(static_cast<unsigned>((cols + b3::LANES - 1) / b3::LANES), static_cast<unsigned>(groups));
-    if (fp2)
-        hipLaunchKernelGGL(b3::column_groups<2>, grid, dim3(b3::LANES), lds, c->stream, m, rows, cols, chunks, group,
-                           groups == 1 ? 1 : 0, gout);
-    else
-        hipLaunchKernelGGL(b3::column_groups<1>, grid, dim3(b3::LANES), lds, c->stream, m, rows, cols, chunks, group,
-                           groups == 1 ? 1 : 0, gout);
+    const dim3 grid(static_cast<unsigned>((cols + b3::LANES - 1) / b3::LANES), static_cast<unsigned>(k));
+    const int is_root = k == 1 ? 1 : 0;
+    uint32_t* gout = k == 1 ? leaves : buf;
+    const bool off32 = cols * w * sizeof(uint64_t) <= 0xFFFFFFFFull;
+    auto launch = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(b3::LANES), 0, c->stream, m, rows, cols, chunks, group, is_root, gout);
+    };
+    if (fp2) off32 ? launch(b3::column_groups<2, true>) : launch(b3::column_groups<2, false>);
+    else off32 ? launch(b3::column_groups<1, true>) : launch(b3::column_groups<1, false>);
     VMX_HIP(c, hipGetLastError());
-    if (groups > 1) {
-        const unsigned threads = groups <= 64 ? 64u : groups <= 128 ? 128u : 256u;
-        hipLaunchKernelGGL(b3::merge_groups, dim3(static_cast<unsigned>(cols)), dim3(threads), 0, c->stream,
-                           static_cast<const uint32_t*>(gout), groups, cols, leaves);
+    const uint32_t* in = buf;
+    uint32_t* next = buf ? buf + k * cols * 8 : nullptr;
+    while (k > 1) {
+        const size_t k_out = (k + b3::FAN_IN - 1) / b3::FAN_IN;
+        const int final = k_out == 1 ? 1 : 0;
+        uint32_t* dst = final ? leaves : next;
+        hipLaunchKernelGGL(b3::merge_pass, dim3(static_cast<unsigned>((cols + b3::LANES - 1) / b3::LANES),
+                                                static_cast<unsigned>(k_out)),
+                           dim3(b3::LANES), 0, c->stream, in, k, cols, final, dst);
         VMX_HIP(c, hipGetLastError());
+        in = dst;
+        next += final ? 0 : k_out * cols * 8;
+        k = k_out;
     }
     return 0;
 }
@@ -408,7 +454,8 @@ int merkle_tree_levels(Context* c, uint32_t* tree, size_t leaves) {
 
 int merkle_paths(Context* c, const uint32_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
                  uint32_t* paths) {
-    const int bits = static_cast<int>(log2_exact(leaves));
+    int bits = 0;
+    while ((size_t{1} << bits) < leaves) ++bits;
     const size_t total = queries * bits;
     hipLaunchKernelGGL(b3::merkle_paths_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0,
                        c->stream, tree, idx, paths, leaves, queries, bits);
