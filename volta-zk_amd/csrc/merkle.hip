@@ -163,7 +163,7 @@ constexpr size_t CHUNK_WORDS = 128; // u64 words per 1024-byte chunk
 // OFF32: a row of the matrix spans less than 4 GiB, so a lane's element is
 // addressed as the uniform row pointer plus a 32-bit byte offset.
 template <int W, bool OFF32>
-__global__ __launch_bounds__(LANES) void column_groups(const uint64_t* __restrict__ m, size_t rows, size_t cols,
+__global__ __launch_bounds__(LANES, 6) void column_groups(const uint64_t* __restrict__ m, size_t rows, size_t cols,
                                                        size_t chunks, size_t group, int root,
                                                        uint32_t* __restrict__ out) {
     const int lane = threadIdx.x;
@@ -219,46 +219,49 @@ __global__ __launch_bounds__(LANES) void column_groups(const uint64_t* __restric
 
     const uint32_t top = root ? PARENT | ROOT : PARENT;  // flags of the group's last join
     uint32_t cv[8], p0[8], p1[8];
-    // compress block k; at a chunk's end fold the chunk into p0 / p1
-    auto step = [&](const uint32_t* mw, size_t k) {
-        const int lc = static_cast<int>(k / 16);  // chunk within the group
-        const int cb = static_cast<int>(k % 16);
-        const bool chunk_end = (cb == 15) || (k + 1 == total);
+    auto compress_block = [&](const uint32_t* mw, size_t k, int cb, int nb) {
         const size_t left = words - (c_begin * 16 + k) * 8;
         const uint32_t len = static_cast<uint32_t>(min<size_t>(8, left) * 8);
-        if (cb == 0)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) cv[i] = IV[i];
-        uint32_t flags = (cb == 0 ? CHUNK_START : 0u) | (chunk_end ? CHUNK_END : 0u);
-        if (chunks == 1 && chunk_end) flags |= ROOT;  // a one-chunk column: this block is the root
-        compress(cv, mw, c_begin + lc, len, flags);
-        if (!chunk_end) return;
-        if (lc == 0) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) p0[i] = cv[i];
-        } else if (lc == 1) {
-            join(p0, p0, cv, n_local == 2 ? top : PARENT);
-        } else if (lc == 2) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) p1[i] = cv[i];
-        } else {
-            join(p1, p1, cv, PARENT);
-            join(p0, p0, p1, top);
-        }
+        uint32_t flags = (cb == 0 ? CHUNK_START : 0u) | (cb + 1 == nb ? CHUNK_END : 0u);
+        if (chunks == 1 && cb + 1 == nb) flags |= ROOT;  // a one-chunk column: this block is the root
+        compress(cv, mw, c_begin + k / 16, len, flags);
     };
 
-    // two buffers: the next block loads while the current one compresses
+    // Two block buffers alternate: the next block loads while the current one
+    // compresses.  A full chunk has 16 blocks, so the next chunk's first block
+    // always lands in `a`; only the column's last chunk can be shorter.
     uint32_t a[16], b[16];
     load_block(0, a);
-    for (size_t k = 0;;) {
-        if (k + 1 < total) load_block(k + 1, b);
-        step(a, k);
-        if (++k == total) break;
-        if (k + 1 < total) load_block(k + 1, a);
-        step(b, k);
-        if (++k == total) break;
+    for (size_t lc = 0; lc < n_local; ++lc) {
+        const size_t k0 = lc * 16;
+        const int nb = static_cast<int>(min<size_t>(16, total - k0));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cv[i] = IV[i];
+        for (int cb = 0; cb < nb; cb += 2) {
+            if (k0 + cb + 1 < total) load_block(k0 + cb + 1, b);
+            compress_block(a, k0 + cb, cb, nb);
+            if (cb + 1 == nb) break;
+            if (k0 + cb + 2 < total) load_block(k0 + cb + 2, a);
+            compress_block(b, k0 + cb + 1, cb + 1, nb);
+        }
+        // chunk lc done: chunks 0 and 2 wait in p0 / p1, chunks 1 and 3 join them
+        if ((lc & 1) == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) (lc == 0 ? p0 : p1)[i] = cv[i];
+        } else {
+            uint32_t l[8], j[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) l[i] = lc == 1 ? p0[i] : p1[i];
+            join(j, l, cv, lc == 1 && n_local == 2 ? top : PARENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) (lc == 1 ? p0 : p1)[i] = j[i];
+        }
     }
-    if (n_local == 3) join(p0, p0, p1, top);
+    if (chunks == 1) {  // the single block chain already carried ROOT
+        store_hash(out + col * 8, cv);
+        return;
+    }
+    if (n_local >= 3) join(p0, p0, p1, top);  // (0+1) + 2  or  (0+1) + (2+3)
     store_hash(out + (root ? col : gi * cols + col) * 8, p0);
 }
 
@@ -309,6 +312,66 @@ __global__ __launch_bounds__(LANES) void merge_pass(const uint32_t* __restrict__
         join(acc, l, acc, PARENT | (depth == 0 && final ? ROOT : 0u));
     }
     store_hash(out + (final ? col : j * cols + col) * 8, acc);
+}
+
+constexpr int MERGE_THREADS = 256;
+constexpr int MERGE_MAX = 2 * MERGE_THREADS;  // values per column merge_final handles
+
+// The column's last fold when it has k_in <= 512 values (in[(i cols + col) 8
+// ..]): the workgroup holds cpw = 256 / tpc columns (tpc = ceil(k_in / 2)
+// rounded up to a power of two) and joins each column's values level by
+// level in LDS, carrying an odd last value up unchanged (which builds the
+// same left-complete tree); the last join carries ROOT.  Each level is one
+// join deep.
+__global__ __launch_bounds__(MERGE_THREADS) void merge_final(const uint32_t* __restrict__ in, int k_in, size_t cols,
+                                                             int cpw, uint32_t* __restrict__ leaves) {
+    __shared__ uint32_t node[MERGE_MAX][9];  // odd pitch: a join reads two neighbouring nodes
+    const int t = threadIdx.x;
+    const int per = MERGE_MAX / cpw;          // node slots per column
+    const int tpc = MERGE_THREADS / cpw;      // threads per column
+    // columns interleave across threads: a level's active threads (r < pairs)
+    // are the first pairs * cpw, packed into as few waves as possible
+    const int q = t % cpw, r = t / cpw;       // column within the workgroup, thread within the column
+    const size_t col = static_cast<size_t>(blockIdx.x) * cpw + q;
+    const bool live = q < cpw && col < cols;
+    uint32_t(*mine)[9] = node + q * per;
+    if (live)
+        for (int i = r; i < k_in; i += tpc) {
+            uint32_t h[8];
+            load_hash(h, in + (static_cast<size_t>(i) * cols + col) * 8);
+#pragma unroll
+            for (int w = 0; w < 8; ++w) mine[i][w] = h[w];
+        }
+    __syncthreads();
+    for (int count = k_in; count > 1;) {
+        const int pairs = count / 2;
+        uint32_t p[8];
+        const bool act = live && r < pairs;
+        if (act) {
+            uint32_t l[8], rr[8];
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                l[w] = mine[2 * r][w];
+                rr[w] = mine[2 * r + 1][w];
+            }
+            join(p, l, rr, PARENT | (count == 2 ? ROOT : 0u));
+        }
+        __syncthreads();
+        if (act)
+#pragma unroll
+            for (int w = 0; w < 8; ++w) mine[r][w] = p[w];
+        if (live && (count & 1) && r == pairs)  // carry the odd last value up unchanged
+#pragma unroll
+            for (int w = 0; w < 8; ++w) mine[pairs][w] = mine[count - 1][w];
+        __syncthreads();
+        count = pairs + (count & 1);
+    }
+    if (live && r == 0) {
+        uint32_t h[8];
+#pragma unroll
+        for (int w = 0; w < 8; ++w) h[w] = mine[0][w];
+        store_hash(leaves + col * 8, h);
+    }
 }
 
 constexpr uint32_t PAIR_FLAGS = CHUNK_START | CHUNK_END | ROOT;  // blake3 of a 64-byte message
@@ -419,17 +482,24 @@ int merkle_column_leaves(Context* c, const uint64_t* m, size_t rows, size_t cols
     VMX_HIP(c, hipGetLastError());
     const uint32_t* in = buf;
     uint32_t* next = buf ? buf + k * cols * 8 : nullptr;
-    while (k > 1) {
+    while (k > static_cast<size_t>(b3::MERGE_MAX)) {  // 16-way passes down to a single workgroup's worth
         const size_t k_out = (k + b3::FAN_IN - 1) / b3::FAN_IN;
-        const int final = k_out == 1 ? 1 : 0;
-        uint32_t* dst = final ? leaves : next;
         hipLaunchKernelGGL(b3::merge_pass, dim3(static_cast<unsigned>((cols + b3::LANES - 1) / b3::LANES),
                                                 static_cast<unsigned>(k_out)),
-                           dim3(b3::LANES), 0, c->stream, in, k, cols, final, dst);
+                           dim3(b3::LANES), 0, c->stream, in, k, cols, 0, next);
         VMX_HIP(c, hipGetLastError());
-        in = dst;
-        next += final ? 0 : k_out * cols * 8;
+        in = next;
+        next += k_out * cols * 8;
         k = k_out;
+    }
+    if (k > 1) {
+        // threads per column: the first level's joins, rounded up to a power of two
+        size_t tpc = 1;
+        while (tpc < (k + 1) / 2) tpc *= 2;
+        const int cpw = static_cast<int>(b3::MERGE_THREADS / tpc);
+        hipLaunchKernelGGL(b3::merge_final, dim3(static_cast<unsigned>((cols + cpw - 1) / cpw)),
+                           dim3(b3::MERGE_THREADS), 0, c->stream, in, static_cast<int>(k), cols, cpw, leaves);
+        VMX_HIP(c, hipGetLastError());
     }
     return 0;
 }
