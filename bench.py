@@ -12,7 +12,9 @@ in HBM before timing starts; outputs stay resident.
 Prints one JSON line: whole-step throughput in codeword Gelem/s, the
 roofline of the dominant kernel (the encode) from HIP events recorded by the
 library on its own stream, and a CPU baseline (the oracle restatement of the
-reference CPU path, OpenMP over the host cores) on the same workload.
+reference CPU path, OpenMP over the host cores) on the same workload.  After
+the timed steps it also times the commit's BLAKE3 column tree over the
+resident codewords (`commit_tree`, reported beside `value`, not in it).
 """
 from __future__ import annotations
 
@@ -160,6 +162,30 @@ def copy_bandwidth(b, nbytes: int = 1 << 32, reps: int = 10) -> float:
     return 2 * nbytes / dt / 1e9
 
 
+def commit_tree(b, wl: Workload, reps: int = 10) -> dict:
+    """BLAKE3 column leaves + Merkle tree over the step's resident codeword
+    matrix (the reference commit's last stage, ligero.rs:595-621), timed with
+    the library's own HIP events after the timed steps; not part of `value`."""
+    import numpy as np
+    rows, n = wl.cfg.rows, wl.cfg.n
+    tree = b.alloc_device((2 * n - 1) * 32, np.uint8)
+    call = lambda: wl._ok(wl.lib.volta_cuda_hash_fp_tree_device(wl.raw, wl.enc.id, 0, rows, n, tree.id, 0))
+    for _ in range(2):
+        call()
+    b.synchronize()
+    b.reset_stats()
+    for _ in range(reps):
+        call()
+    b.synchronize()
+    s = b.get_stats()
+    b.free_device(tree)
+    ms = s["kernel_ns"]["pcs_merkle"] / max(s["calls"]["pcs_merkle"], 1) / 1e6
+    matrix = rows * n * 8
+    return {"kernel": "BLAKE3 column leaves + Merkle tree (volta_cuda_hash_fp_tree_device)",
+            "rows": rows, "leaves": n, "ms_per_tree": round(ms, 4), "matrix_bytes": matrix,
+            "achieved_gbs": round(matrix / ms / 1e6, 1), "reps": reps}
+
+
 def cpu_baseline(name: str, wl: Workload) -> dict:
     """The oracle's restatement of the reference CPU path (per-row radix-2 DIT
     NttPlan::forward + combine_rows), OpenMP over this host's cores."""
@@ -222,6 +248,7 @@ def main() -> int:
     ap.add_argument("--config", default="c3", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-copy-probe", action="store_true")
+    ap.add_argument("--no-commit-tree", action="store_true")
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -252,6 +279,10 @@ def main() -> int:
     launches_per_step = max(enc_calls // a.steps, 1)
     alg = cfg.algorithmic_bytes  # per encode launch (C5: one direction)
     achieved = alg / enc_s / 1e9 if enc_s > 0 else None
+    tree = None
+    if not a.no_commit_tree and a.config != "c5":
+        log("commit tree over the codewords")
+        tree = commit_tree(b, wl)
     copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
     wl_close = wl.close
     cpu = None
@@ -290,6 +321,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "kernel_ms_per_step": {k: round(v / a.steps / 1e6, 4) for k, v in stats["kernel_ns"].items() if v},
+        "commit_tree": tree,
     }
     print(json.dumps(out), flush=True)
     return 0
