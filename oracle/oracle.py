@@ -88,6 +88,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "vo_fnv_u64": (u64, [vp, sz, u64]),
         "vo_fp2_mul_stream": (None, [vp, vp, vp, sz, i32]),
         "vo_fp2_chain": (None, [vp, vp, vp, sz, i32, i32]),
+        "vo_eq_rows": (None, [vp, sz, sz, vp]),
+        "vo_fp2_row_dots": (None, [vp, sz, vp, sz, sz, sz, vp]),
         "vo_blake3": (None, [vp, sz, vp]),
         "vo_hash_fp_columns": (None, [vp, sz, sz, vp, i32]),
         "vo_hash_fp2_columns": (None, [vp, sz, sz, vp, i32]),
@@ -342,6 +344,24 @@ def fp2_chain(a, b, rounds: int, threads: int | None = None) -> np.ndarray:
     out = np.empty_like(a)
     lib().vo_fp2_chain(_ptr(a), _ptr(b), _ptr(out), a.size, rounds,
                        threads or default_threads())
+    return fp2_to_u64(out)
+
+
+# ---- opening-path helpers ------------------------------------------------------------------
+
+def eq_rows(points, rows: int, dims: int) -> np.ndarray:
+    """rows x 2^dims x 2: prod_k (bit k of x ? p_k : 1 - p_k) per row."""
+    pts = _fp2_array(np.asarray(points, dtype=np.uint64).reshape(rows * dims, 2) if dims else np.zeros((1, 2), np.uint64))
+    out = np.zeros(rows << dims, FP2_DTYPE)
+    lib().vo_eq_rows(_ptr(pts), rows, dims, _ptr(out))
+    return fp2_to_u64(out).reshape(rows, 1 << dims, 2)
+
+
+def fp2_row_dots(a, a_stride: int, b, b_stride: int, rows: int, length: int) -> np.ndarray:
+    """rows x 2: sum_j a[r a_stride + j] b[r b_stride + j]."""
+    a, b = _fp2_array(a).reshape(-1), _fp2_array(b).reshape(-1)
+    out = np.zeros(rows, FP2_DTYPE)
+    lib().vo_fp2_row_dots(_ptr(a), a_stride, _ptr(b), b_stride, rows, length, _ptr(out))
     return fp2_to_u64(out)
 
 

@@ -315,6 +315,38 @@ void vo_gather_fp2_columns(const vo_fp2* m, size_t rows, size_t cols, const uint
         for (size_t i = 0; i < rows; ++i) out[q * rows + i] = m[i * cols + idx[q]];
 }
 
+/* Equality rows for the opening's claim and mask points
+ * (volta_cuda_logup_eq_rows_device, cuda/volta_cuda_backend.cu:6884-6911 with
+ * eq_rows_expand .cu:2860-2871; callers rust/volta-accel/src/lib.rs:3037-3053,
+ * 6167-6205): out[r][x] = prod_k (bit k of x ? p[r][k] : 1 - p[r][k]) for
+ * x < 2^dims, written here as the direct product. */
+void vo_eq_rows(const vo_fp2* points, size_t rows, size_t dims, vo_fp2* out) {
+    const size_t width = (size_t)1 << dims;
+    const vo_fp2 one = {1, 0};
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t x = 0; x < width; ++x) {
+            vo_fp2 acc = one;
+            for (size_t k = 0; k < dims; ++k) {
+                const vo_fp2 p = points[r * dims + k];
+                const vo_fp2 f = ((x >> k) & 1) ? p : (vo_fp2){vo_fp_sub(1, p.c0), vo_fp_sub(0, p.c1)};
+                acc = vo_fp2_mul(acc, f);
+            }
+            out[r * width + x] = acc;
+        }
+}
+
+/* out[r] = sum_j a[r a_stride + j] b[r b_stride + j] for j < len
+ * (volta_cuda_fp2_row_dots_device, .cu:1374-1391, 4049-4103; caller
+ * Backend::fp2_row_dots_device, rust/volta-accel/src/lib.rs:1873-1908). */
+void vo_fp2_row_dots(const vo_fp2* a, size_t a_stride, const vo_fp2* b, size_t b_stride, size_t rows, size_t len,
+                     vo_fp2* out) {
+    for (size_t r = 0; r < rows; ++r) {
+        vo_fp2 acc = {0, 0};
+        for (size_t j = 0; j < len; ++j) acc = vo_fp2_add(acc, vo_fp2_mul(a[r * a_stride + j], b[r * b_stride + j]));
+        out[r] = acc;
+    }
+}
+
 /* ------------------------------------------------------------------------ */
 /* ChaCha8 FpStream                                                          */
 /* ------------------------------------------------------------------------ */

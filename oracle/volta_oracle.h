@@ -115,6 +115,14 @@ void vo_fp2_mul_stream(const vo_fp2* a, const vo_fp2* b, vo_fp2* out, size_t n, 
 void vo_fp2_chain(const vo_fp2* a, const vo_fp2* b, vo_fp2* out, size_t n, int rounds,
                   int threads);
 
+/* ---- opening-path helpers ------------------------------------------------ */
+/* out[r][x] = prod_k (bit k of x ? p[r][k] : 1 - p[r][k]), x < 2^dims
+ * (cuda/volta_cuda_backend.cu:2860-2871, 6884-6911) */
+void vo_eq_rows(const vo_fp2* points, size_t rows, size_t dims, vo_fp2* out);
+/* out[r] = sum_j a[r a_stride + j] b[r b_stride + j] (.cu:1374-1391) */
+void vo_fp2_row_dots(const vo_fp2* a, size_t a_stride, const vo_fp2* b, size_t b_stride, size_t rows,
+                     size_t len, vo_fp2* out);
+
 /* ---- BLAKE3 column leaves and Merkle tree (volta_oracle_blake3.c) -------
  * blake3 1.8.5 (rust/Cargo.lock:51-53) restated from the BLAKE3 specification;
  * merkle.rs:9-51, ligero.rs:595-621. Hashes are 32 bytes. */

@@ -306,3 +306,82 @@ def test_coarse_timing_scope_and_wall_only_policy():
         assert s["coarse_timing_scopes"] == 1
         b.free_device(d)
         b.free_device(o2)
+
+
+# ---- opening-path helpers ----------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,dims", [(1, 0), (3, 1), (2, 3), (4, 4), (5, 7), (2, 12), (1, 18)])
+def test_eq_rows_match_oracle(backend, oracle, rows, dims):
+    from volta_mi355x import FP2
+    pts = rand_fp(rows * 100 + dims, (rows * dims, 2)) if dims else None
+    dp = backend.upload_device(pts, FP2) if dims else None
+    out = backend.logup_eq_rows_device(dp, rows, dims)
+    got = backend.download_device(out).view(np.uint64).reshape(rows, 1 << dims, 2)
+    backend.free_device(out)
+    if dp is not None:
+        backend.free_device(dp)
+    want = oracle.eq_rows(pts if dims else np.zeros((0, 2), np.uint64), rows, dims)
+    assert (got == want).all()
+
+
+def test_equality_weights_and_row_dots_evaluate_an_mle(backend, oracle):
+    """The opening's use (ligero.rs:1300-1400): eq weights of a point dotted
+    with a row give the row's multilinear extension at that point."""
+    from volta_mi355x import FP2
+    dims, rows = 6, 3
+    point = rand_fp(41, (dims, 2))
+    weights = backend.equality_weights_device(point)
+    vals = rand_fp(42, (rows * 80, 2))  # rows of 64 values at stride 80
+    dv = backend.alloc_device(rows * 80, FP2)
+    backend.upload_into(dv, 0, vals.reshape(-1))
+    # b stride 0 is not allowed (stride >= len): replicate the weights per row
+    w = backend.download_device(weights).view(np.uint64).reshape(-1, 2)
+    dw = backend.upload_device(np.tile(w, (rows, 1)), FP2)
+    out = backend.fp2_row_dots_device(dv, 0, 80, dw, 0, 64, rows, 64)
+    got = backend.download_device(out).view(np.uint64).reshape(rows, 2)
+    for x in (weights, dv, dw, out):
+        backend.free_device(x)
+    assert (w.reshape(1, 64, 2) == oracle.eq_rows(point, 1, dims)).all()
+    assert (got == oracle.fp2_row_dots(vals, 80, np.tile(w, (rows, 1)), 64, rows, 64)).all()
+
+    # independent of the table: fold row 0 by the coordinates, LSB first,
+    # f'(y) = f(2y) (1 - p_k) + f(2y + 1) p_k, in big integers
+    def mul(a, b):
+        return ((a[0] * b[0] + 7 * a[1] * b[1]) % P, (a[0] * b[1] + a[1] * b[0]) % P)
+
+    f = [(int(v[0]), int(v[1])) for v in vals[:64]]
+    for k in range(dims):
+        pk = (int(point[k][0]), int(point[k][1]))
+        one_minus = ((1 - pk[0]) % P, (-pk[1]) % P)
+        f = [tuple((x + y) % P for x, y in zip(mul(f[2 * i], one_minus), mul(f[2 * i + 1], pk)))
+             for i in range(len(f) // 2)]
+    assert tuple(int(v) for v in got[0]) == f[0]
+
+
+@pytest.mark.parametrize("rows,length,sa,sb,a_off", [(1, 1, 1, 1, 0), (7, 300, 301, 310, 5), (40, 2048, 2048, 4096, 0),
+                                                      (3, 70000, 70000, 70000, 1)])
+def test_fp2_row_dots_match_oracle(backend, oracle, rows, length, sa, sb, a_off):
+    from volta_mi355x import FP2
+    a = rand_fp(rows + length, (a_off + (rows - 1) * sa + length, 2))
+    b = rand_fp(rows * 3 + length, ((rows - 1) * sb + length, 2))
+    da, db = backend.upload_device(a, FP2), backend.upload_device(b, FP2)
+    out = backend.fp2_row_dots_device(da, a_off, sa, db, 0, sb, rows, length)
+    got = backend.download_device(out).view(np.uint64).reshape(rows, 2)
+    for x in (da, db, out):
+        backend.free_device(x)
+    assert (got == oracle.fp2_row_dots(a[a_off:], sa, b, sb, rows, length)).all()
+
+
+def test_opening_helper_errors(backend):
+    from volta_mi355x import FP2
+    lib, raw = backend.lib, backend.raw
+    a = backend.alloc_device(64, FP2)
+    # output overlapping an input
+    assert lib.volta_cuda_fp2_row_dots_device(raw, a.id, 0, 8, a.id, 0, 8, a.id, 2, 2, 8) != 0
+    assert "overlaps" in backend.last_error()
+    assert lib.volta_cuda_fp2_row_dots_device(raw, a.id, 0, 4, a.id, 0, 8, a.id, 40, 2, 8) != 0  # stride < len
+    assert "geometry" in backend.last_error()
+    assert lib.volta_cuda_logup_eq_rows_device(raw, 0, 0, 1, 3, a.id, 0) != 0  # dims without points
+    assert "geometry" in backend.last_error()
+    assert lib.volta_cuda_logup_eq_rows_device(raw, a.id, 0, 1, 8, a.id, 0) != 0  # 256 outputs > 64 slots
+    backend.free_device(a)

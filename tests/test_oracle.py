@@ -302,3 +302,54 @@ def test_merkle_paths_verify_and_detect_tampering(oracle):
             assert not _verify_path(oracle, root, i ^ 1, leaves[i].tobytes(), path)
         bad = oracle.merkle_paths(tree, n, np.array([n, n + 5], np.uint32))
         assert not bad.any()  # out-of-range queries read as zero hashes
+
+
+# ---- opening-path helpers -------------------------------------------------------------
+
+def _f2mul(a, b):
+    """(a0 + a1 phi)(b0 + b1 phi) with phi^2 = 7 (rust/volta-field/src/lib.rs:173-177)."""
+    return ((a[0] * b[0] + 7 * a[1] * b[1]) % P, (a[0] * b[1] + a[1] * b[0]) % P)
+
+
+def test_eq_rows_boolean_points_are_indicators(oracle):
+    """A 0/1 point selects exactly the index whose bit k is coordinate k: pins
+    the LSB-first bit order of the reference's expansion (.cu:2860-2871)."""
+    dims = 4
+    pts = np.array([[(x >> k) & 1, 0] for x in (0, 5, 10, 15) for k in range(dims)], np.uint64)
+    eq = oracle.eq_rows(pts, 4, dims)
+    for r, x in enumerate((0, 5, 10, 15)):
+        want = np.zeros((1 << dims, 2), np.uint64)
+        want[x, 0] = 1
+        assert (eq[r] == want).all()
+
+
+def test_eq_rows_against_big_ints_and_sum_to_one(oracle):
+    rnd = random.Random(11)
+    rows, dims = 3, 5
+    pts = [(rnd.randrange(P), rnd.randrange(P)) for _ in range(rows * dims)]
+    eq = oracle.eq_rows(np.array(pts, np.uint64), rows, dims)
+    for r in range(rows):
+        total = (0, 0)
+        for x in range(1 << dims):
+            acc = (1, 0)
+            for k in range(dims):
+                p = pts[r * dims + k]
+                acc = _f2mul(acc, p if (x >> k) & 1 else ((1 - p[0]) % P, (-p[1]) % P))
+            assert tuple(int(v) for v in eq[r, x]) == acc
+            total = ((total[0] + acc[0]) % P, (total[1] + acc[1]) % P)
+        assert total == (1, 0)  # sum_x eq(p, x) = prod_k (p_k + 1 - p_k) = 1
+    assert (oracle.eq_rows(np.zeros((0, 2), np.uint64), 2, 0) == np.array([[[1, 0]], [[1, 0]]])).all()
+
+
+def test_fp2_row_dots_against_big_ints(oracle):
+    rnd = np.random.default_rng(12)
+    rows, length, sa, sb = 4, 37, 40, 37
+    a = rnd.integers(0, P, size=(rows * sa, 2), dtype=np.uint64)
+    b = rnd.integers(0, P, size=(rows * sb, 2), dtype=np.uint64)
+    got = oracle.fp2_row_dots(a, sa, b, sb, rows, length)
+    for r in range(rows):
+        acc = (0, 0)
+        for j in range(length):
+            t = _f2mul(tuple(int(v) for v in a[r * sa + j]), tuple(int(v) for v in b[r * sb + j]))
+            acc = ((acc[0] + t[0]) % P, (acc[1] + t[1]) % P)
+        assert tuple(int(v) for v in got[r]) == acc

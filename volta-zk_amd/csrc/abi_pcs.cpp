@@ -661,3 +661,66 @@ VMX_API int volta_cuda_hash_fp_columns(void* raw, const uint64_t* matrix, size_t
         return finish_op(c, OP_PCS_MERKLE, mb, hb);
     });
 }
+
+// ---------------------------------------------------------------------------
+// Opening-path helpers
+// ---------------------------------------------------------------------------
+
+// Replaces volta_cuda_logup_eq_rows_device (.cu:6884-6911; callers
+// Backend::logup_eq_rows_device and equality_weights_device,
+// rust/volta-accel/src/lib.rs:6167-6205, 3037-3053): rows x 2^dims Fp2,
+// out[r][x] = prod_k (bit k of x ? p[r][k] : 1 - p[r][k]).  dims = 0 writes
+// one 1 per row and reads no points.
+VMX_API int volta_cuda_logup_eq_rows_device(void* raw, uint64_t points_id, size_t points_off, size_t rows,
+                                               size_t dims, uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || dims >= 63 || (dims && !points_id)) return fail_msg(c, "invalid resident eq-row geometry");
+    return guarded(c, "resident eq rows", [&] {
+        const size_t width = size_t{1} << dims;
+        size_t total = 0, pn = 0;
+        if (!mul_ok(rows, width, &total) || !mul_ok(rows, dims, &pn))
+            return fail_msg(c, "resident eq-row geometry overflows size_t");
+        void *points = nullptr, *out = nullptr;
+        if ((dims && region_elems(c, points_id, points_off, pn, 16, &points)) ||
+            region_elems(c, out_id, out_off, total, 16, &out))
+            return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (eq_rows(c, static_cast<const Fp2*>(points), rows, dims, static_cast<Fp2*>(out))) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_LOGUP, 0, 0);
+    });
+}
+
+// Replaces volta_cuda_fp2_row_dots_device (.cu:4049-4103; caller
+// Backend::fp2_row_dots_device, rust/volta-accel/src/lib.rs:1873-1908):
+// out[r] = sum_{j < len} a[r a_stride + j] b[r b_stride + j], element offsets
+// and strides; the output may not overlap either input.
+VMX_API int volta_cuda_fp2_row_dots_device(void* raw, uint64_t a_id, size_t a_off, size_t a_stride, uint64_t b_id,
+                                              size_t b_off, size_t b_stride, uint64_t out_id, size_t out_off,
+                                              size_t rows, size_t len) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !len || a_stride < len || b_stride < len) return fail_msg(c, "invalid Fp2 row-dot geometry");
+    return guarded(c, "Fp2 row dots", [&] {
+        size_t aob = 0, asb = 0, bob = 0, bsb = 0, rowb = 0;
+        if (!mul_ok(a_off, 16, &aob) || !mul_ok(a_stride, 16, &asb) || !mul_ok(b_off, 16, &bob) ||
+            !mul_ok(b_stride, 16, &bsb) || !mul_ok(len, 16, &rowb))
+            return fail_msg(c, "Fp2 row-dot geometry overflows size_t");
+        void *a = nullptr, *b = nullptr, *out = nullptr;
+        size_t a_span = 0, b_span = 0;
+        if (strided_region(c, a_id, aob, asb, rowb, rows, &a, &a_span) ||
+            strided_region(c, b_id, bob, bsb, rowb, rows, &b, &b_span) ||
+            region_elems(c, out_id, out_off, rows, 16, &out))
+            return -1;
+        auto overlaps = [&](const void* p, size_t n) {
+            const char *o = static_cast<const char*>(out), *q = static_cast<const char*>(p);
+            return o < q + n && q < o + rows * 16;
+        };
+        if (overlaps(a, a_span) || overlaps(b, b_span)) return fail_msg(c, "Fp2 row-dot output overlaps an input");
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (fp2_row_dots(c, static_cast<const Fp2*>(a), a_stride, static_cast<const Fp2*>(b), b_stride,
+                         static_cast<Fp2*>(out), rows, len))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}

@@ -28,10 +28,6 @@ static int vmx_out_of_scope(void* raw, const char* name) {
     return -1;
 }
 
-VMX_API int volta_cuda_fp2_row_dots_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, size_t a8, size_t a9, size_t a10) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8, (void)a9, (void)a10; return vmx_out_of_scope(ctx, "volta_cuda_fp2_row_dots_device");
-}
-
 VMX_API int volta_cuda_gemm_i64(void* ctx, const int16_t* a1, const int16_t* a2, int64_t* a3, size_t a4, size_t a5, size_t a6) {
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_gemm_i64");
 }
@@ -310,10 +306,6 @@ VMX_API int volta_cuda_logup_suffix_eq_device(void* ctx, uint64_t a1, size_t a2,
 
 VMX_API int volta_cuda_fp2_fold_rows_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, VoltaFp2 a5, uint64_t a6, size_t a7) {
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7; return vmx_out_of_scope(ctx, "volta_cuda_fp2_fold_rows_device");
-}
-
-VMX_API int volta_cuda_logup_eq_rows_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_logup_eq_rows_device");
 }
 
 VMX_API int volta_cuda_logup_aux_round_device(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, uint64_t a5, size_t a6, uint64_t a7, size_t a8, uint64_t a9, size_t a10, uint64_t a11, size_t a12, uint64_t a13, size_t a14, size_t a15, size_t a16, size_t a17, VoltaFp2 a18, VoltaFp2 a19, VoltaFp2 a20, VoltaFp2* a21) {

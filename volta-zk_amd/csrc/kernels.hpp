@@ -46,6 +46,12 @@ int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, si
 int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows,
                             size_t count, size_t padded, gl::Fp2* out);
 
+// Opening-path helpers: equality rows (rows x 2^dims, LSB-first) and strided
+// Fp2 row dot products.
+int eq_rows(Context* c, const gl::Fp2* points, size_t rows, size_t dims, gl::Fp2* out);
+int fp2_row_dots(Context* c, const gl::Fp2* a, size_t a_stride, const gl::Fp2* b, size_t b_stride, gl::Fp2* out,
+                 size_t rows, size_t len);
+
 // BLAKE3 column leaves of a rows x cols Fp (fp2 = false) or Fp2 matrix into
 // leaves[cols][8 words]; the Merkle levels above cols leaves stored after
 // them (tree = leaves, then each level, root last); sibling paths.

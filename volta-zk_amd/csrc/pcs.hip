@@ -533,3 +533,112 @@ int probe_fp2_chain(Context* c, const Fp2* a, const Fp2* b, Fp2* out, size_t n, 
 }
 
 }  // namespace vmx
+
+namespace vmx {
+
+// ---- opening-path helpers -------------------------------------------------------------------
+
+namespace {
+
+__device__ __forceinline__ Fp2 fp2_one_minus(Fp2 p) { return Fp2{gl::sub(1, p.c0), gl::neg(p.c1)}; }
+__device__ __forceinline__ Fp2 fp2_sub(Fp2 a, Fp2 b) { return Fp2{gl::sub(a.c0, b.c0), gl::sub(a.c1, b.c1)}; }
+
+// out[r][x] = prod_k (bit k of x ? p[r][k] : 1 - p[r][k]) for x < 2^dims
+// (reference eq_rows_expand, .cu:2860-2871).  Thread (r, hi) owns the 2^LOW
+// consecutive x = hi 2^LOW + i: one product over the high bits, then the low
+// bits expanded in registers from the highest down, v -> (v - v p, v p), which
+// is the reference's expansion order; two products per output.
+template <int LOW>
+__global__ __launch_bounds__(256) void eq_rows_kernel(const Fp2* __restrict__ points, size_t rows, int dims,
+                                                      Fp2* __restrict__ out) {
+    const size_t per_row = size_t{1} << (dims - LOW);
+    const size_t total = rows * per_row;
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < total; z += stride) {
+        const size_t r = z / per_row, hi = z - r * per_row;
+        const Fp2* p = points + r * dims;
+        Fp2 v[1 << LOW];
+        v[0] = Fp2{1, 0};
+        for (int k = LOW; k < dims; ++k) {
+            const Fp2 pk = p[k];
+            v[0] = gl::fp2_mul(v[0], ((hi >> (k - LOW)) & 1) ? pk : fp2_one_minus(pk));
+        }
+#pragma unroll
+        for (int k = LOW - 1; k >= 0; --k) {
+            const Fp2 pk = p[k];
+            const int cnt = 1 << (LOW - 1 - k);
+#pragma unroll
+            for (int i = cnt - 1; i >= 0; --i) {
+                const Fp2 t = gl::fp2_mul(v[i], pk);
+                const Fp2 s = fp2_sub(v[i], t);
+                v[2 * i + 1] = t;
+                v[2 * i] = s;
+            }
+        }
+        Fp2* o = out + (r << dims) + (hi << LOW);
+#pragma unroll
+        for (int i = 0; i < (1 << LOW); ++i) o[i] = v[i];
+    }
+}
+
+constexpr int DOT_THREADS = 256;
+
+__device__ __forceinline__ Fp2 fp2_shfl_xor(Fp2 x, int m) {
+    const uint64_t c0 = __shfl_xor(x.c0, m), c1 = __shfl_xor(x.c1, m);
+    return Fp2{c0, c1};
+}
+
+// out[r] = sum_j a[r a_stride + j] b[r b_stride + j] (reference .cu:1374-1391):
+// one workgroup per row, strided partial sums, a shuffle reduction inside each
+// wave and one LDS step across the four waves.
+__global__ __launch_bounds__(DOT_THREADS) void fp2_row_dots_kernel(const Fp2* __restrict__ a, size_t a_stride,
+                                                                   const Fp2* __restrict__ b, size_t b_stride,
+                                                                   Fp2* __restrict__ out, size_t rows, size_t len) {
+    __shared__ Fp2 part[DOT_THREADS / 64];
+    const int t = threadIdx.x;
+    for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        Fp2 acc{0, 0};
+        for (size_t j = t; j < len; j += DOT_THREADS)
+            acc = gl::fp2_add(acc, gl::fp2_mul(a[row * a_stride + j], b[row * b_stride + j]));
+#pragma unroll
+        for (int m = 32; m > 0; m >>= 1) acc = gl::fp2_add(acc, fp2_shfl_xor(acc, m));
+        if ((t & 63) == 0) part[t >> 6] = acc;
+        __syncthreads();
+        if (t == 0) {
+            Fp2 s = part[0];
+#pragma unroll
+            for (int w = 1; w < DOT_THREADS / 64; ++w) s = gl::fp2_add(s, part[w]);
+            out[row] = s;
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+int eq_rows(Context* c, const Fp2* points, size_t rows, size_t dims, Fp2* out) {
+    const int d = static_cast<int>(dims);
+    const int low = d < 4 ? d : 4;
+    const size_t threads = rows << (dims - low);
+    const dim3 grid(grid_for(threads, 256, 1 << 16));
+    switch (low) {
+        case 0: hipLaunchKernelGGL(eq_rows_kernel<0>, grid, dim3(256), 0, c->stream, points, rows, d, out); break;
+        case 1: hipLaunchKernelGGL(eq_rows_kernel<1>, grid, dim3(256), 0, c->stream, points, rows, d, out); break;
+        case 2: hipLaunchKernelGGL(eq_rows_kernel<2>, grid, dim3(256), 0, c->stream, points, rows, d, out); break;
+        case 3: hipLaunchKernelGGL(eq_rows_kernel<3>, grid, dim3(256), 0, c->stream, points, rows, d, out); break;
+        default: hipLaunchKernelGGL(eq_rows_kernel<4>, grid, dim3(256), 0, c->stream, points, rows, d, out); break;
+    }
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+int fp2_row_dots(Context* c, const Fp2* a, size_t a_stride, const Fp2* b, size_t b_stride, Fp2* out, size_t rows,
+                 size_t len) {
+    const unsigned blocks = static_cast<unsigned>(rows < 65535 ? rows : 65535);
+    hipLaunchKernelGGL(fp2_row_dots_kernel, dim3(blocks), dim3(DOT_THREADS), 0, c->stream, a, a_stride, b, b_stride,
+                       out, rows, len);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+}  // namespace vmx

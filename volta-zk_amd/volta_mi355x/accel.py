@@ -125,6 +125,8 @@ _SIGS = {
     "volta_cuda_pcs_combine_rows": (_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, _vp]),
     "volta_cuda_fp2_powers_device": (_int, [_vp, _u64, _u64, _u64, _sz, _sz]),
     "volta_cuda_fp2_add_inplace_device": (_int, [_vp, _u64, _sz, _u64, _sz, _sz]),
+    "volta_cuda_logup_eq_rows_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
+    "volta_cuda_fp2_row_dots_device": (_int, [_vp, _u64, _sz, _sz, _u64, _sz, _sz, _u64, _sz, _sz, _sz]),
     "volta_cuda_pcs_gather_columns_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz, _sz, _u64, _sz, _int]),
     "volta_cuda_pcs_gather_columns": (_int, [_vp, _vp, _sz, _sz, _vp, _sz, _vp]),
     "volta_cuda_chacha8_prover_secret_fp_rows_device": (_int, [_vp, _u64, _sz, _vp, _u64, _sz, _sz]),
@@ -543,6 +545,42 @@ class Backend:
         return out
 
     # ---- helpers ---------------------------------------------------------------------------
+    # ---- opening-path helpers (lib.rs:1873-1908, 3037-3053, 6167-6205) -------------------
+    def logup_eq_rows_device(self, points: DeviceBuffer | None, rows: int, dims: int) -> DeviceBuffer:
+        """rows x 2^dims Fp2: row r is the LSB-first equality table of point r."""
+        if rows == 0 or dims >= 64:
+            raise InvalidInput("invalid resident eq-row geometry")
+        if dims and points is None:
+            raise InvalidInput("non-empty equality rows require resident points")
+        if points is not None:
+            self._region(points, 0, rows * dims)
+        out = self.alloc_device(rows << dims, FP2)
+        self._call_or_free(out, self.lib.volta_cuda_logup_eq_rows_device, points.id if points is not None else 0, 0,
+                           rows, dims, out.id, 0)
+        return out
+
+    def equality_weights_device(self, point) -> DeviceBuffer:
+        """The 2^len(point) equality weights of one Fp2 point (lib.rs:3037-3053)."""
+        pts = np.ascontiguousarray(point, dtype=np.uint64).reshape(-1, 2)
+        buf = self.upload_device(pts, FP2) if len(pts) else None
+        try:
+            return self.logup_eq_rows_device(buf, 1, len(pts))
+        finally:
+            if buf is not None:
+                self.free_device(buf)
+
+    def fp2_row_dots_device(self, a: DeviceBuffer, a_offset: int, a_stride: int, b: DeviceBuffer, b_offset: int,
+                            b_stride: int, rows: int, length: int) -> DeviceBuffer:
+        """rows Fp2: sum_j a[r a_stride + j] b[r b_stride + j] (element offsets)."""
+        if rows == 0 or length == 0 or a_stride < length or b_stride < length:
+            raise InvalidInput("invalid Fp2 row-dot geometry")
+        self._region(a, a_offset, (rows - 1) * a_stride + length)
+        self._region(b, b_offset, (rows - 1) * b_stride + length)
+        out = self.alloc_device(rows, FP2)
+        self._call_or_free(out, self.lib.volta_cuda_fp2_row_dots_device, a.id, a_offset, a_stride, b.id, b_offset,
+                           b_stride, out.id, 0, rows, length)
+        return out
+
     # ---- BLAKE3 column leaves and Merkle tree (lib.rs:6380-6405, 6677-6770) ------------
     def _hash_tree_device(self, matrix: DeviceBuffer, rows: int, cols: int, fp2: bool) -> DeviceMerkleTree:
         if rows == 0 or cols == 0 or cols & (cols - 1):
