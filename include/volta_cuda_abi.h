@@ -18,9 +18,10 @@
  * that return host data synchronise.  A context is not thread-safe (the Rust
  * owner serialises calls through &mut).
  *
- * Symbols marked "out of scope here" belong to the reference's GEMM, LogUp,
- * X4 and Merkle subsystems; they are exported with their exact signatures so
- * the loader resolves them, and fail explicitly when called.
+ * Symbols marked "out of scope here" belong to the reference's GEMM,
+ * fixed-point inference, LogUp and X4c arena/session subsystems; they are
+ * exported with their exact signatures so the loader resolves them, and fail
+ * explicitly when called.
  */
 #ifndef VOLTA_CUDA_ABI_H
 #define VOLTA_CUDA_ABI_H
@@ -152,8 +153,8 @@ int volta_cuda_chacha8_prover_secret_fp_rows_device(void* ctx, uint64_t out_id, 
 int volta_cuda_mock_correlation_sub_masks_device(void* ctx, uint64_t out_id, size_t out_off_bytes, const uint8_t* seed, uint64_t base, size_t rows, size_t cols);
 /* rust/volta-accel/src/cuda.rs:156 (type Chacha8ProverSecretFp2RowsPaddedDevice), loaded at cuda.rs:1220; MI355X implementation. */
 int volta_cuda_chacha8_prover_secret_fp2_rows_padded_device(void* ctx, uint64_t out_id, size_t out_off_bytes, const uint8_t* seed, uint64_t base, size_t rows, size_t count, size_t padded);
-/* rust/volta-accel/src/cuda.rs:158 (type Fp2RowDotsDevice), loaded at cuda.rs:1223; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_fp2_row_dots_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, size_t a8, size_t a9, size_t a10);
+/* rust/volta-accel/src/cuda.rs:158 (type Fp2RowDotsDevice), loaded at cuda.rs:1223; MI355X implementation. */
+int volta_cuda_fp2_row_dots_device(void* ctx, uint64_t a_id, size_t a_off, size_t a_stride, uint64_t b_id, size_t b_off, size_t b_stride, uint64_t out_id, size_t out_off, size_t rows, size_t len);
 /* rust/volta-accel/src/cuda.rs:171 (type Fp2PowersDevice), loaded at cuda.rs:1225; MI355X implementation. */
 int volta_cuda_fp2_powers_device(void* ctx, uint64_t c0, uint64_t c1, uint64_t out_id, size_t out_off, size_t count);
 /* rust/volta-accel/src/cuda.rs:172 (type GemmI64), loaded at cuda.rs:1226; out of scope here: returns -1 with a last_error message. */
@@ -252,8 +253,8 @@ int volta_cuda_ntt_fp(void* ctx, const uint64_t* msg, size_t msg_len, size_t n, 
 int volta_cuda_ntt_fp_batch(void* ctx, const uint64_t* msgs, size_t rows, size_t msg_len, size_t n, uint64_t* out);
 /* rust/volta-accel/src/cuda.rs:676 (type NttFp2), loaded at cuda.rs:1347; MI355X implementation. */
 int volta_cuda_ntt_fp2(void* ctx, const VoltaFp2* msg, size_t msg_len, size_t n, VoltaFp2* out);
-/* rust/volta-accel/src/cuda.rs:676 (type NttFp2), loaded at cuda.rs:1348; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_x4b_ntt_fp2(void* ctx, const VoltaFp2* a1, size_t a2, size_t a3, VoltaFp2* a4);
+/* rust/volta-accel/src/cuda.rs:676 (type NttFp2), loaded at cuda.rs:1348; MI355X implementation. */
+int volta_cuda_x4b_ntt_fp2(void* ctx, const VoltaFp2* coefficients, size_t coefficient_len, size_t n, VoltaFp2* output);
 /* rust/volta-accel/src/cuda.rs:679 (type X4bContextProbe), loaded at cuda.rs:1349; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_x4b_context_probe(void* ctx, const uint8_t* a1, size_t a2, uint8_t* a3);
 /* rust/volta-accel/src/cuda.rs:680 (type X4bN4InnerTile), loaded at cuda.rs:1350; out of scope here: returns -1 with a last_error message. */
@@ -264,8 +265,8 @@ int volta_cuda_x4b_n4_outer_nodes(void* ctx, const uint8_t* a1, size_t a2, uint6
 int volta_cuda_x4c_direct_fold_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, size_t a7, size_t a8, uint64_t a9, uint64_t a10);
 /* rust/volta-accel/src/cuda.rs:709 (type X4cUploadPinned), loaded at cuda.rs:1355; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_x4c_upload_pinned(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5);
-/* rust/volta-accel/src/cuda.rs:710 (type X4cDirectFoldArena), loaded at cuda.rs:1357; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_x4c_direct_fold_arena(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, uint64_t a6);
+/* rust/volta-accel/src/cuda.rs:710 (type X4cDirectFoldArena), loaded at cuda.rs:1357; MI355X implementation. */
+int volta_cuda_x4c_direct_fold_arena(void* ctx, uint64_t arena_id, size_t input_offset_bytes, size_t input_len, size_t output_offset_bytes, uint64_t challenge_c0, uint64_t challenge_c1);
 /* rust/volta-accel/src/cuda.rs:712 (type X4cActivationAddPinnedTile), loaded at cuda.rs:1360; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_x4c_activation_add_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, uint64_t a7, uint64_t a8);
 /* rust/volta-accel/src/cuda.rs:714 (type X4cBuildOneSlotN4), loaded at cuda.rs:1363; out of scope here: returns -1 with a last_error message. */
@@ -306,8 +307,8 @@ int volta_cuda_fp2_deinterleave_device(void* ctx, uint64_t a1, size_t a2, size_t
 int volta_cuda_logup_suffix_eq_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5);
 /* rust/volta-accel/src/cuda.rs:838 (type Fp2FoldRowsDevice), loaded at cuda.rs:1407; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_fp2_fold_rows_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, VoltaFp2 a5, uint64_t a6, size_t a7);
-/* rust/volta-accel/src/cuda.rs:840 (type LogupEqRowsDevice), loaded at cuda.rs:1410; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_logup_eq_rows_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6);
+/* rust/volta-accel/src/cuda.rs:840 (type LogupEqRowsDevice), loaded at cuda.rs:1410; MI355X implementation. */
+int volta_cuda_logup_eq_rows_device(void* ctx, uint64_t points_id, size_t points_off, size_t rows, size_t dims, uint64_t out_id, size_t out_off);
 /* rust/volta-accel/src/cuda.rs:842 (type LogupAuxRoundDevice), loaded at cuda.rs:1413; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_logup_aux_round_device(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, uint64_t a5, size_t a6, uint64_t a7, size_t a8, uint64_t a9, size_t a10, uint64_t a11, size_t a12, uint64_t a13, size_t a14, size_t a15, size_t a16, size_t a17, VoltaFp2 a18, VoltaFp2 a19, VoltaFp2 a20, VoltaFp2* a21);
 /* rust/volta-accel/src/cuda.rs:866 (type LogupAuxRoundIntoDevice), loaded at cuda.rs:1416; out of scope here: returns -1 with a last_error message. */
@@ -316,24 +317,24 @@ int volta_cuda_logup_aux_round_into_device(void* ctx, uint64_t a1, size_t a2, ui
 int volta_cuda_pcs_combine_rows(void* ctx, const int16_t* weights, const uint64_t* pads, const VoltaFp2* coeffs, size_t rows, size_t cols, size_t pad, size_t combinations, VoltaFp2* out);
 /* rust/volta-accel/src/cuda.rs:903 (type PcsGatherColumns), loaded at cuda.rs:1419; MI355X implementation. */
 int volta_cuda_pcs_gather_columns(void* ctx, const uint64_t* matrix, size_t rows, size_t cols, const uint32_t* idx, size_t queries, uint64_t* out);
-/* rust/volta-accel/src/cuda.rs:891 (type HashFpColumns), loaded at cuda.rs:1420; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_hash_fp_columns(void* ctx, const uint64_t* a1, size_t a2, size_t a3, uint8_t* a4);
+/* rust/volta-accel/src/cuda.rs:891 (type HashFpColumns), loaded at cuda.rs:1420; MI355X implementation. */
+int volta_cuda_hash_fp_columns(void* ctx, const uint64_t* matrix, size_t rows, size_t cols, uint8_t* leaves);
 /* rust/volta-accel/src/cuda.rs:912 (type PcsMessagesDevice), loaded at cuda.rs:1422; MI355X implementation. */
 int volta_cuda_pcs_messages_device(void* ctx, uint64_t w_id, size_t w_off, uint64_t pads_id, size_t pads_off, size_t rows, size_t cols, size_t pad, size_t code_len, uint64_t out_id, size_t out_off);
 /* rust/volta-accel/src/cuda.rs:925 (type PcsCombineRowsDevice), loaded at cuda.rs:1425; MI355X implementation. */
 int volta_cuda_pcs_combine_rows_device(void* ctx, uint64_t w_id, size_t w_off, uint64_t pads_id, size_t pads_off, uint64_t co_id, size_t co_off, size_t rows, size_t cols, size_t pad, size_t combinations, uint64_t out_id, size_t out_off);
 /* rust/volta-accel/src/cuda.rs:940 (type Fp2AddInplaceDevice), loaded at cuda.rs:1428; MI355X implementation. */
 int volta_cuda_fp2_add_inplace_device(void* ctx, uint64_t t_id, size_t t_off, uint64_t a_id, size_t a_off, size_t n);
-/* rust/volta-accel/src/cuda.rs:942 (type Fp2MobiusInverseInplaceDevice), loaded at cuda.rs:1431; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_fp2_mobius_inverse_inplace_device(void* ctx, uint64_t a1, size_t a2, size_t a3);
+/* rust/volta-accel/src/cuda.rs:942 (type Fp2MobiusInverseInplaceDevice), loaded at cuda.rs:1431; MI355X implementation. */
+int volta_cuda_fp2_mobius_inverse_inplace_device(void* ctx, uint64_t values_id, size_t values_offset, size_t n);
 /* rust/volta-accel/src/cuda.rs:943 (type Fp2AffineEqWeightsInplaceDevice), loaded at cuda.rs:1434; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_fp2_affine_eq_weights_inplace_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, uint64_t a8, uint64_t a9, uint64_t a10);
-/* rust/volta-accel/src/cuda.rs:956 (type HashTreeDevice), loaded at cuda.rs:1437; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_hash_fp_tree_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6);
-/* rust/volta-accel/src/cuda.rs:956 (type HashTreeDevice), loaded at cuda.rs:1440; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_hash_fp2_tree_device(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, size_t a6);
-/* rust/volta-accel/src/cuda.rs:958 (type MerklePathsDevice), loaded at cuda.rs:1443; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_merkle_paths_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, size_t a8);
+/* rust/volta-accel/src/cuda.rs:956 (type HashTreeDevice), loaded at cuda.rs:1437; MI355X implementation. */
+int volta_cuda_hash_fp_tree_device(void* ctx, uint64_t matrix_id, size_t matrix_off, size_t rows, size_t cols, uint64_t tree_id, size_t tree_off_bytes);
+/* rust/volta-accel/src/cuda.rs:956 (type HashTreeDevice), loaded at cuda.rs:1440; MI355X implementation. */
+int volta_cuda_hash_fp2_tree_device(void* ctx, uint64_t matrix_id, size_t matrix_off, size_t rows, size_t cols, uint64_t tree_id, size_t tree_off_bytes);
+/* rust/volta-accel/src/cuda.rs:958 (type MerklePathsDevice), loaded at cuda.rs:1443; MI355X implementation. */
+int volta_cuda_merkle_paths_device(void* ctx, uint64_t tree_id, size_t tree_off_bytes, size_t leaves, uint64_t idx_id, size_t idx_off, size_t queries, uint64_t paths_id, size_t paths_off_bytes);
 /* rust/volta-accel/src/cuda.rs:960 (type PcsGatherColumnsDevice), loaded at cuda.rs:1446; MI355X implementation. */
 int volta_cuda_pcs_gather_columns_device(void* ctx, uint64_t m_id, size_t m_off, size_t rows, size_t cols, uint64_t idx_id, size_t idx_off, size_t queries, uint64_t out_id, size_t out_off, int fp2);
 
@@ -366,6 +367,14 @@ int volta_mi355x_pcs_encode_device(void* ctx, uint64_t w_id, size_t w_off, uint6
 int volta_mi355x_combine_rows_fp_device(void* ctx, uint64_t m_id, size_t m_off, size_t rows, size_t cols,
                                         uint64_t coeffs_id, size_t coeffs_off, size_t combinations,
                                         uint64_t out_id, size_t out_off);
+
+/* The X4 Fp2 NTT of volta_cuda_x4b_ntt_fp2 on resident buffers (element
+ * offsets): in[in_off .. in_off + len) (zero beyond len) -> out[out_off ..
+ * out_off + n), natural order, n a power of two in [2, 2^33].  The regions must
+ * not overlap; the input is left unchanged.  The reference's X4 NTT takes host
+ * pointers only (cuda/volta_cuda_backend.cu:5577-5634). */
+int volta_mi355x_x4_ntt_fp2_device(void* ctx, uint64_t in_id, size_t in_off, size_t len, size_t n, uint64_t out_id,
+                                   size_t out_off);
 
 /* Device address of a resident byte region / the context stream (a
  * hipStream_t), so a harness can time launches with its own events. */

@@ -30,11 +30,31 @@ class Fp2C(ctypes.Structure):
     _fields_ = [("c0", ctypes.c_uint64), ("c1", ctypes.c_uint64)]
 
 
+def _stale() -> bool:
+    if not _LIB_PATH.exists():
+        return True
+    built = _LIB_PATH.stat().st_mtime
+    return any(p.stat().st_mtime > built for p in _HERE.glob("volta_oracle*.[ch]"))
+
+
 def build(force: bool = False) -> None:
-    """Compile liboracle.so with the committed Makefile."""
-    if force or not _LIB_PATH.exists():
+    """Compile liboracle.so with the committed Makefile (again when a source is newer)."""
+    if force or _stale():
         subprocess.run(["make", "-B" if force else "-s", "-C", str(_HERE)], check=True,
                        stdout=subprocess.DEVNULL)
+
+
+REFERENCE = pathlib.Path("/root/reference")
+
+
+def build_reference() -> bool:
+    """Compile oracle/_ref (the reference's X4 host sources, `make ref`) when
+    the reference checkout exists; returns whether it was built."""
+    if not (REFERENCE / "cuda" / "volta_x4b.cuh").exists():
+        return False
+    subprocess.run(["make", "-s", "-B", "-C", str(_HERE), "ref", "REF=" + str(REFERENCE)], check=True,
+                   stdout=subprocess.DEVNULL)
+    return True
 
 
 _lib = None
@@ -96,6 +116,15 @@ def _declare(L: ctypes.CDLL) -> None:
         "vo_merkle_tree": (None, [vp, sz, vp]),
         "vo_merkle_paths": (None, [vp, sz, vp, sz, vp]),
         "vo_merkle_bench_matrix": (None, [sz, sz, vp, i32]),
+        "vo_fp2_pow": (Fp2C, [Fp2C, u64]),
+        "vo_fp2_inv": (Fp2C, [Fp2C]),
+        "vo_x4_root_of_unity": (Fp2C, [ctypes.c_uint32]),
+        "vo_x4_ntt": (None, [vp, sz, sz, vp]),
+        "vo_x4_fold_codeword": (None, [vp, sz, Fp2C, vp]),
+        "vo_x4_fold_coefficients": (None, [vp, sz, Fp2C, vp]),
+        "vo_fp2_mobius": (None, [vp, sz, i32]),
+        "vo_mle_eval_coefficients": (Fp2C, [vp, sz, vp, sz]),
+        "vo_mle_eval_table": (Fp2C, [vp, sz, vp, sz]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -418,3 +447,66 @@ def merkle_bench_matrix(rows: int, cols: int, threads: int | None = None) -> np.
     out = np.zeros(rows * cols, np.uint64)
     lib().vo_merkle_bench_matrix(rows, cols, _ptr(out), threads or default_threads())
     return out
+
+
+# ---- X4 extension-field transforms (volta_oracle_x4.c) ----------------------------------
+
+def _c(x) -> Fp2C:
+    return Fp2C(int(x[0]), int(x[1]))
+
+
+def _t(r: Fp2C) -> tuple:
+    return (r.c0, r.c1)
+
+
+def fp2_pow(a, e: int) -> tuple: return _t(lib().vo_fp2_pow(_c(a), e))
+def fp2_inv(a) -> tuple: return _t(lib().vo_fp2_inv(_c(a)))
+
+
+def x4_root_of_unity(bits: int) -> tuple:
+    """The X4 domain root of order 2^bits, bits <= 33 (x4/ntt.rs:49-57)."""
+    return _t(lib().vo_x4_root_of_unity(bits))
+
+
+def x4_ntt(coeffs, n: int) -> np.ndarray:
+    """n x 2: Fp2NttPlan(n).encode(coeffs) (x4/ntt.rs:66-122)."""
+    c = _fp2_array(np.asarray(coeffs, dtype=np.uint64).reshape(-1, 2))
+    assert 1 <= c.size <= n and n >= 2 and n & (n - 1) == 0
+    out = np.zeros(n, FP2_DTYPE)
+    lib().vo_x4_ntt(_ptr(c), c.size, n, _ptr(out))
+    return fp2_to_u64(out)
+
+
+def x4_fold_codeword(values, challenge) -> np.ndarray:
+    """n/2 x 2: fold_codeword(values, challenge) (x4/ntt.rs:238-256)."""
+    v = _fp2_array(np.asarray(values, dtype=np.uint64).reshape(-1, 2))
+    out = np.zeros(v.size // 2, FP2_DTYPE)
+    lib().vo_x4_fold_codeword(_ptr(v), v.size, _c(challenge), _ptr(out))
+    return fp2_to_u64(out)
+
+
+def x4_fold_coefficients(coeffs, challenge) -> np.ndarray:
+    """n/2 x 2: c[2j] + challenge c[2j+1] (x4/ntt.rs:230-235)."""
+    v = _fp2_array(np.asarray(coeffs, dtype=np.uint64).reshape(-1, 2))
+    out = np.zeros(v.size // 2, FP2_DTYPE)
+    lib().vo_x4_fold_coefficients(_ptr(v), v.size, _c(challenge), _ptr(out))
+    return fp2_to_u64(out)
+
+
+def fp2_mobius(values, inverse: bool) -> np.ndarray:
+    """Moebius transform (inverse=False: evaluations -> coefficients) (x4/ntt.rs:147-188)."""
+    v = _fp2_array(np.array(values, dtype=np.uint64).reshape(-1, 2))
+    lib().vo_fp2_mobius(_ptr(v), v.size, 1 if inverse else 0)
+    return fp2_to_u64(v)
+
+
+def mle_eval_coefficients(coeffs, point) -> tuple:
+    c = _fp2_array(np.asarray(coeffs, dtype=np.uint64).reshape(-1, 2))
+    pt = _fp2_array(np.asarray(point, dtype=np.uint64).reshape(-1, 2))
+    return _t(lib().vo_mle_eval_coefficients(_ptr(c), c.size, _ptr(pt), pt.size))
+
+
+def mle_eval_table(table, point) -> tuple:
+    t = _fp2_array(np.asarray(table, dtype=np.uint64).reshape(-1, 2))
+    pt = _fp2_array(np.asarray(point, dtype=np.uint64).reshape(-1, 2))
+    return _t(lib().vo_mle_eval_table(_ptr(t), t.size, _ptr(pt), pt.size))

@@ -134,6 +134,18 @@ void vo_merkle_paths(const uint8_t* tree, size_t leaves, const uint32_t* idx, si
                      uint8_t* paths);                                          /* merkle.rs:43-51 */
 void vo_merkle_bench_matrix(size_t rows, size_t cols, uint64_t* m, int threads); /* p7_blake3_merkle.cu:243 */
 
+/* ---- X4 extension-field transforms (volta_oracle_x4.c) -------------------
+ * rust/volta-pcs/src/x4/ntt.rs; cuda/volta_x4b.cuh. */
+vo_fp2 vo_fp2_pow(vo_fp2 base, uint64_t e);                                   /* ntt.rs:15-26 */
+vo_fp2 vo_fp2_inv(vo_fp2 a);                                                   /* volta_x4b.cuh:107-115 */
+vo_fp2 vo_x4_root_of_unity(uint32_t bits);                                     /* ntt.rs:28-57 */
+void vo_x4_ntt(const vo_fp2* coeffs, size_t len, size_t n, vo_fp2* out);      /* ntt.rs:66-122 */
+void vo_x4_fold_codeword(const vo_fp2* v, size_t n, vo_fp2 challenge, vo_fp2* out); /* ntt.rs:238-256 */
+void vo_x4_fold_coefficients(const vo_fp2* c, size_t n, vo_fp2 challenge, vo_fp2* out); /* ntt.rs:230-235 */
+void vo_fp2_mobius(vo_fp2* v, size_t n, int inverse);                          /* ntt.rs:147-188 */
+vo_fp2 vo_mle_eval_coefficients(const vo_fp2* c, size_t n, const vo_fp2* point, size_t dims); /* ntt.rs:190-207 */
+vo_fp2 vo_mle_eval_table(const vo_fp2* t, size_t n, const vo_fp2* point, size_t dims);        /* ntt.rs:209-228 */
+
 #ifdef __cplusplus
 }
 #endif

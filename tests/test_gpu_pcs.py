@@ -247,7 +247,9 @@ def test_geometry_and_id_errors(backend):
     assert "reserved correlation bits" in backend.last_error()
     assert lib.volta_cuda_chacha8_prover_secret_fp_rows_device(raw, out.id, 0, seed, 0, 0, 1) != 0
     # out-of-scope symbols fail explicitly
-    assert lib.volta_cuda_fp2_mobius_inverse_inplace_device(raw, out.id, 0, 1) != 0
+    import ctypes
+    assert lib.volta_cuda_x4c_arena_reset(raw, ctypes.c_uint64(out.id), ctypes.c_size_t(0), ctypes.c_size_t(16),
+                                          ctypes.c_int(0)) != 0
     assert "not implemented" in backend.last_error()
     backend.free_device(again)
     backend.free_device(out)

@@ -724,3 +724,131 @@ VMX_API int volta_cuda_fp2_row_dots_device(void* raw, uint64_t a_id, size_t a_of
         return finish_op(c, OP_PCS_ROWS, 0, 0);
     });
 }
+
+// ---------------------------------------------------------------------------
+// X4 extension-field transforms
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr size_t X4_MAX_N = size_t{1} << 33;
+
+int log2_of(size_t n) {
+    int b = 0;
+    while ((size_t{1} << b) < n) ++b;
+    return b;
+}
+
+bool x4_fold_geometry(size_t input_len, uint64_t c0, uint64_t c1) {
+    return pow2(input_len) && input_len <= X4_MAX_N && c0 < gl::P && c1 < gl::P;
+}
+
+}  // namespace
+
+// Replaces volta_cuda_x4b_ntt_fp2 (cuda/volta_cuda_backend.cu:5577-5634): the
+// n-point NTT of the coefficients (zero beyond coefficient_len) with the X4
+// root of order n (rust/volta-pcs/src/x4/ntt.rs:49-122), natural order.  The
+// coefficient tail is zero-filled inside the transform's first pass (the
+// stats still report it as zeroed bytes, as the reference's memset does); the
+// X4 tables are uploaded once per size and counted as H2D bytes.
+VMX_API int volta_cuda_x4b_ntt_fp2(void* raw, const Fp2* coefficients, size_t coefficient_len, size_t n,
+                                   Fp2* output) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !coefficients || !output || !coefficient_len || coefficient_len > n || !pow2(n) || n > X4_MAX_N)
+        return fail_msg(c, "invalid X4b Fp2 NTT geometry");
+    return guarded(c, "X4b Fp2 NTT", [&] {
+        size_t total = 0, in_bytes = 0;
+        if (!mul_ok(n, sizeof(Fp2), &total) || !mul_ok(coefficient_len, sizeof(Fp2), &in_bytes))
+            return fail_msg(c, "X4b Fp2 NTT byte geometry overflows size_t");
+        if (ensure_ws(c, WS_IN, in_bytes) || ensure_ws(c, WS_OUT, total)) return -1;
+        uint64_t h2d = 0;
+        X4Tables tb;
+        if (x4_tables(c, log2_of(n), &h2d, &tb)) return -1;
+        if (begin_op(c)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), coefficients, in_bytes, hipMemcpyHostToDevice, c->stream));
+        h2d += in_bytes;
+        if (mark_op(c, 1)) return -1;
+        if (x4_ntt(c, tb, ws<Fp2>(c, WS_IN), coefficient_len, ws<Fp2>(c, WS_OUT))) return -1;
+        if (mark_op(c, 2)) return -1;
+        VMX_HIP(c, hipMemcpyAsync(output, ws<Fp2>(c, WS_OUT), total, hipMemcpyDeviceToHost, c->stream));
+        return finish_op(c, OP_PCS_NTT, h2d, total, 0, total - in_bytes);
+    });
+}
+
+// MI355X extension: the same X4 NTT on resident buffers (element offsets):
+// in[in_off .. in_off + len) -> out[out_off .. out_off + n).  The regions must
+// not overlap; the input is left unchanged.
+VMX_API int volta_mi355x_x4_ntt_fp2_device(void* raw, uint64_t in_id, size_t in_off, size_t len, size_t n,
+                                           uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !len || len > n || !pow2(n) || n > X4_MAX_N) return fail_msg(c, "invalid resident X4 NTT geometry");
+    return guarded(c, "resident X4 NTT", [&] {
+        void *in = nullptr, *out = nullptr;
+        if (region_elems(c, in_id, in_off, len, sizeof(Fp2), &in) ||
+            region_elems(c, out_id, out_off, n, sizeof(Fp2), &out))
+            return -1;
+        const auto a = reinterpret_cast<uintptr_t>(in), b = reinterpret_cast<uintptr_t>(out);
+        if (a < b + n * sizeof(Fp2) && b < a + len * sizeof(Fp2))
+            return fail_msg(c, "resident X4 NTT input and output overlap");
+        uint64_t h2d = 0;
+        X4Tables tb;
+        if (x4_tables(c, log2_of(n), &h2d, &tb)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (x4_ntt(c, tb, static_cast<const Fp2*>(in), len, static_cast<Fp2*>(out))) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_NTT, h2d, 0);
+    });
+}
+
+// Replaces volta_cuda_x4c_direct_fold_arena (.cu:5925-5972): the codeword of
+// input_len Fp2 at input_offset_bytes of the arena (a resident buffer) folds
+// into input_len/2 Fp2 at output_offset_bytes (fold_codeword,
+// rust/volta-pcs/src/x4/ntt.rs:238-256).
+VMX_API int volta_cuda_x4c_direct_fold_arena(void* raw, uint64_t arena_id, size_t input_offset_bytes,
+                                             size_t input_len, size_t output_offset_bytes, uint64_t challenge_c0,
+                                             uint64_t challenge_c1) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !x4_fold_geometry(input_len, challenge_c0, challenge_c1))
+        return fail_msg(c, "invalid X4c arena direct-fold geometry");
+    return guarded(c, "X4c arena direct fold", [&] {
+        const size_t half = input_len / 2;
+        size_t in_bytes = 0, out_bytes = 0;
+        if (!mul_ok(input_len, sizeof(Fp2), &in_bytes) || !mul_ok(half, sizeof(Fp2), &out_bytes))
+            return fail_msg(c, "X4c arena direct-fold byte geometry overflows size_t");
+        // 16 bytes: the reference's alignof(volta_x4b::Fp2)
+        if ((input_offset_bytes | output_offset_bytes) % 16 != 0)
+            return fail_msg(c, "misaligned X4c arena direct-fold region");
+        void *in = nullptr, *out = nullptr;
+        if (region(c, arena_id, input_offset_bytes, in_bytes, &in) ||
+            region(c, arena_id, output_offset_bytes, out_bytes, &out))
+            return -1;
+        if (input_offset_bytes < output_offset_bytes + out_bytes && output_offset_bytes < input_offset_bytes + in_bytes)
+            return fail_msg(c, "X4c arena direct-fold input/output overlap");
+        uint64_t h2d = 0;
+        X4Tables tb;
+        if (x4_tables(c, log2_of(input_len), &h2d, &tb)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        const Fp2* pos = static_cast<const Fp2*>(in);
+        if (x4_fold(c, tb, pos, pos + half, static_cast<Fp2*>(out), 0, half, Fp2{challenge_c0, challenge_c1}))
+            return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, h2d, 0, 0, 0, out_bytes);
+    });
+}
+
+// Replaces volta_cuda_fp2_mobius_inverse_inplace_device (.cu:2965-2972,
+// 7114-7130): for every bit of the index, upper += lower, over n = 2^k Fp2 at
+// values_offset (elements) of the resident buffer.
+VMX_API int volta_cuda_fp2_mobius_inverse_inplace_device(void* raw, uint64_t values_id, size_t values_offset,
+                                                         size_t n) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !n || (n & (n - 1))) return fail_msg(c, "invalid resident Fp2 Mobius inverse");
+    return guarded(c, "resident Fp2 Mobius inverse", [&] {
+        void* v = nullptr;
+        if (region_elems(c, values_id, values_offset, n, sizeof(Fp2), &v)) return -1;
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (fp2_mobius(c, static_cast<Fp2*>(v), n, true)) return -1;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, 0, 0);
+    });
+}

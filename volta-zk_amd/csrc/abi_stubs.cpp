@@ -208,10 +208,6 @@ VMX_API int volta_cuda_deinterleave_base_columns_device(void* ctx, uint64_t a1, 
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_deinterleave_base_columns_device");
 }
 
-VMX_API int volta_cuda_x4b_ntt_fp2(void* ctx, const VoltaFp2* a1, size_t a2, size_t a3, VoltaFp2* a4) {
-    (void)a1, (void)a2, (void)a3, (void)a4; return vmx_out_of_scope(ctx, "volta_cuda_x4b_ntt_fp2");
-}
-
 VMX_API int volta_cuda_x4b_context_probe(void* ctx, const uint8_t* a1, size_t a2, uint8_t* a3) {
     (void)a1, (void)a2, (void)a3; return vmx_out_of_scope(ctx, "volta_cuda_x4b_context_probe");
 }
@@ -230,10 +226,6 @@ VMX_API int volta_cuda_x4c_direct_fold_pinned_tile(void* ctx, uint64_t a1, size_
 
 VMX_API int volta_cuda_x4c_upload_pinned(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5) {
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5; return vmx_out_of_scope(ctx, "volta_cuda_x4c_upload_pinned");
-}
-
-VMX_API int volta_cuda_x4c_direct_fold_arena(void* ctx, uint64_t a1, size_t a2, size_t a3, size_t a4, uint64_t a5, uint64_t a6) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6; return vmx_out_of_scope(ctx, "volta_cuda_x4c_direct_fold_arena");
 }
 
 VMX_API int volta_cuda_x4c_activation_add_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, uint64_t a7, uint64_t a8) {
@@ -314,10 +306,6 @@ VMX_API int volta_cuda_logup_aux_round_device(void* ctx, uint64_t a1, size_t a2,
 
 VMX_API int volta_cuda_logup_aux_round_into_device(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, uint64_t a5, size_t a6, uint64_t a7, size_t a8, uint64_t a9, size_t a10, uint64_t a11, size_t a12, uint64_t a13, size_t a14, size_t a15, size_t a16, size_t a17, VoltaFp2 a18, VoltaFp2 a19, VoltaFp2 a20, uint64_t a21, size_t a22) {
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8, (void)a9, (void)a10, (void)a11, (void)a12, (void)a13, (void)a14, (void)a15, (void)a16, (void)a17, (void)a18, (void)a19, (void)a20, (void)a21, (void)a22; return vmx_out_of_scope(ctx, "volta_cuda_logup_aux_round_into_device");
-}
-
-VMX_API int volta_cuda_fp2_mobius_inverse_inplace_device(void* ctx, uint64_t a1, size_t a2, size_t a3) {
-    (void)a1, (void)a2, (void)a3; return vmx_out_of_scope(ctx, "volta_cuda_fp2_mobius_inverse_inplace_device");
 }
 
 VMX_API int volta_cuda_fp2_affine_eq_weights_inplace_device(void* ctx, uint64_t a1, size_t a2, size_t a3, uint64_t a4, size_t a5, size_t a6, uint64_t a7, uint64_t a8, uint64_t a9, uint64_t a10) {

@@ -204,6 +204,36 @@ int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out) {
     return 0;
 }
 
+int ensure_split_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out) {
+    TwiddleSet& t = c->twiddles[n];
+    t.n = n;
+    if (!t.split) {
+        if (c->coarse_active) return reject(c, "twiddle upload is forbidden inside a coarse timing scope");
+        const int bits = tw_log2(n);
+        const int h = (bits + 1) / 2;
+        const size_t lo = size_t{1} << h, hi = n >> h;
+        std::vector<uint64_t> host(lo + hi);
+        const uint64_t w = gl::root_of_unity(static_cast<unsigned>(bits));
+        uint64_t acc = 1;
+        for (size_t i = 0; i < lo; ++i) {
+            host[i] = acc;
+            acc = gl::mul(acc, w);
+        }
+        // acc = w^(2^h) now
+        const uint64_t step = acc;
+        acc = 1;
+        for (size_t i = 0; i < hi; ++i) {
+            host[lo + i] = acc;
+            acc = gl::mul(acc, step);
+        }
+        if (upload_table(c, host, &t.split, h2d)) return -1;
+        t.split_h = h;
+        t.split_bytes = host.size() * sizeof(uint64_t);
+    }
+    *out = &t;
+    return 0;
+}
+
 int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out) {
     TwiddleSet* t = nullptr;
     if (ensure_twiddles(c, n, h2d, &t)) return -1;
@@ -673,6 +703,7 @@ VMX_API void volta_cuda_destroy(void* raw) {
             if (kv.second.fwd) (void)hipFree(kv.second.fwd);
             if (kv.second.inv) (void)hipFree(kv.second.inv);
             if (kv.second.grid) (void)hipFree(kv.second.grid);
+            if (kv.second.split) (void)hipFree(kv.second.split);
         }
         for (auto& p : c->pinned) {
             if (p.ready) (void)hipEventDestroy(p.ready);
@@ -871,7 +902,7 @@ VMX_API int volta_cuda_memory_breakdown(void* raw, uint64_t* workspace, uint64_t
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) w += half;
         if (kv.second.inv) w += half;
-        w += kv.second.grid_bytes;
+        w += kv.second.grid_bytes + kv.second.split_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;
@@ -1244,7 +1275,7 @@ VMX_API int volta_cuda_x4c_control_state(void* raw, RawX4cControlState* out) {
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) r.workspace_device_bytes += half;
         if (kv.second.inv) r.workspace_device_bytes += half;
-        r.workspace_device_bytes += kv.second.grid_bytes;
+        r.workspace_device_bytes += kv.second.grid_bytes + kv.second.split_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;

@@ -188,6 +188,11 @@ struct TwiddleSet {
     uint64_t* inv = nullptr;  // w^0 .. w^-(n/2-1) (inverse transform only)
     uint64_t* grid = nullptr; // w^(i2*j1) laid out for the fast encode (device-built)
     size_t grid_bytes = 0;
+    // Two-level table of w^e for any e < n: lo[j] = w^j (j < 2^h), then
+    // hi[j] = w^(j 2^h) (j < n / 2^h), h = ceil(log2 n / 2); w^e = lo[e & (2^h-1)] hi[e >> h].
+    uint64_t* split = nullptr;
+    size_t split_bytes = 0;
+    int split_h = 0;
     size_t n = 0;
 };
 
@@ -260,6 +265,8 @@ T* ws(Context* c, int slot) {
 // bytes to *h2d (the reference's per-size upload, .cu:2675-2689).
 int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
 int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
+// Two-level table of w^e for size n (TwiddleSet::split), uploaded once.
+int ensure_split_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
 // Device-built table of `bytes` for the fast encode, derived from t->fwd on
 // the device (no host upload).  `build` enqueues the kernel that fills it.
 int ensure_grid_twiddles(Context* c, TwiddleSet* t, size_t bytes, int (*build)(Context*, TwiddleSet*));

@@ -60,6 +60,26 @@ int merkle_tree_levels(Context* c, uint32_t* tree, size_t leaves);
 int merkle_paths(Context* c, const uint32_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
                  uint32_t* paths);
 
+// X4 extension-field transforms (x4.hip).  Tables for transforms and folds of
+// 2^nb points, nb in [1, 33]; uploaded once per size (adds to *h2d), so call
+// before the primitive's timing begins.
+struct X4Tables {
+    const uint64_t* inner = nullptr;  // w_4096^j, j < 2048
+    const uint64_t* split = nullptr;  // two-level table of b_min(nb,32)
+    int split_h = 0;
+    int nb = 0;
+};
+int x4_tables(Context* c, int nb, uint64_t* h2d, X4Tables* out);
+// 2^nb-point X4 Fp2 NTT of the len coefficients at in (zero beyond len) into
+// out (2^nb elements, natural order; must not overlap in).
+int x4_ntt(Context* c, const X4Tables& tb, const gl::Fp2* in, uint64_t len, gl::Fp2* out);
+// Codeword fold of a 2^nb codeword: out[j] for absolute index j0 + j, j < count,
+// from pos[j] = v[j0 + j] and neg[j] = v[j0 + j + 2^(nb-1)].
+int x4_fold(Context* c, const X4Tables& tb, const gl::Fp2* pos, const gl::Fp2* neg, gl::Fp2* out, uint64_t j0,
+            uint64_t count, gl::Fp2 ch);
+// In-place Moebius transform of n = 2^k values (inverse: upper += lower).
+int fp2_mobius(Context* c, gl::Fp2* values, uint64_t n, bool inverse);
+
 // Measurement probes.
 int probe_copy(Context* c, const void* src, void* dst, size_t bytes);
 int probe_fp2_stream(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n);

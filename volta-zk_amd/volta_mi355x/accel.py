@@ -136,6 +136,10 @@ _SIGS = {
     "volta_cuda_hash_fp2_tree_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
     "volta_cuda_merkle_paths_device": (_int, [_vp, _u64, _sz, _sz, _u64, _sz, _sz, _u64, _sz]),
     "volta_cuda_hash_fp_columns": (_int, [_vp, _vp, _sz, _sz, _vp]),
+    "volta_cuda_x4b_ntt_fp2": (_int, [_vp, _vp, _sz, _sz, _vp]),
+    "volta_cuda_x4c_direct_fold_arena": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _u64]),
+    "volta_cuda_fp2_mobius_inverse_inplace_device": (_int, [_vp, _u64, _sz, _sz]),
+    "volta_mi355x_x4_ntt_fp2_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_ntt_fp_inverse_batch_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_ntt_fp_encode_device": (_int, [_vp, _u64, _sz, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_pcs_encode_device": (_int, [_vp, _u64, _sz, _u64, _sz, _sz, _sz, _sz, _sz, _u64, _sz]),
@@ -626,6 +630,57 @@ class Backend:
         out = np.empty((cols, 32), np.uint8)
         self._check(self.lib.volta_cuda_hash_fp_columns(self.raw, m.ctypes.data, rows, cols, out.ctypes.data))
         return out
+
+    # ---- X4 extension-field transforms (lib.rs:4761-4780, 5028-5075, 6601-6620) ---------
+    def x4b_ntt_fp2(self, coefficients, size: int) -> np.ndarray:
+        """size x 2: the X4 Fp2 NTT of the coefficients (x4/ntt.rs:66-122), host form."""
+        cf = _as_fp2(coefficients)
+        if cf.size == 0 or cf.size > size or not self._pow2(size) or size > 1 << 33:
+            raise InvalidInput("invalid X4b Fp2 NTT geometry")
+        out = np.empty(size, dtype=FP2)
+        self._check(self.lib.volta_cuda_x4b_ntt_fp2(self.raw, cf.ctypes.data, cf.size, size, out.ctypes.data))
+        return fp2_as_u64(out)
+
+    def x4_ntt_fp2_device(self, inp: DeviceBuffer, length: int, size: int, out: DeviceBuffer | None = None,
+                          in_offset: int = 0, out_offset: int = 0) -> DeviceBuffer:
+        """The same transform on resident buffers (MI355X extension); allocates out if absent."""
+        if length == 0 or length > size or not self._pow2(size) or size > 1 << 33:
+            raise InvalidInput("invalid resident X4 NTT geometry")
+        self._region(inp, in_offset, length)
+        if out is None:
+            out = self.alloc_device(size, FP2)
+            self._call_or_free(out, self.lib.volta_mi355x_x4_ntt_fp2_device, inp.id, in_offset, length, size, out.id,
+                               out_offset)
+            return out
+        self._region(out, out_offset, size)
+        self._check(self.lib.volta_mi355x_x4_ntt_fp2_device(self.raw, inp.id, in_offset, length, size, out.id,
+                                                            out_offset))
+        return out
+
+    def x4c_direct_fold_arena_into_arena(self, arena: DeviceBuffer, input_offset_bytes: int, input_len: int,
+                                         output_offset_bytes: int, challenge) -> None:
+        """Fold the input_len codeword at input_offset_bytes into input_len/2 Fp2 at
+        output_offset_bytes of the same arena (lib.rs:5028-5075)."""
+        self._own(arena)
+        c0, c1 = (int(challenge[0]), int(challenge[1]))
+        if input_len < 2 or not self._pow2(input_len) or input_len > 1 << 33 or c0 >= P or c1 >= P:
+            raise InvalidInput("invalid X4c direct-fold geometry")
+        in_bytes, out_bytes = input_len * 16, input_len // 2 * 16
+        for off, nb in ((input_offset_bytes, in_bytes), (output_offset_bytes, out_bytes)):
+            if off % 16 or off + nb > arena.nbytes:
+                raise InvalidInput("misaligned or out-of-bounds X4c direct-fold region")
+        if input_offset_bytes < output_offset_bytes + out_bytes and output_offset_bytes < input_offset_bytes + in_bytes:
+            raise InvalidInput("X4c direct-fold input and output overlap")
+        self._check(self.lib.volta_cuda_x4c_direct_fold_arena(self.raw, arena.id, input_offset_bytes, input_len,
+                                                              output_offset_bytes, c0, c1))
+
+    def fp2_mobius_inverse_inplace_device(self, values: DeviceBuffer, offset: int = 0, n: int | None = None) -> None:
+        """For every index bit, upper += lower (lib.rs:6601-6620)."""
+        n = values.len - offset if n is None else n
+        if n == 0 or n & (n - 1):
+            raise InvalidInput("invalid resident Fp2 Mobius inverse")
+        self._region(values, offset, n)
+        self._check(self.lib.volta_cuda_fp2_mobius_inverse_inplace_device(self.raw, values.id, offset, n))
 
     def _call_or_free(self, out: DeviceBuffer, fn, *args) -> None:
         rc = fn(self.raw, *args)
