@@ -14,7 +14,9 @@ roofline of the dominant kernel (the encode) from HIP events recorded by the
 library on its own stream, and a CPU baseline (the oracle restatement of the
 reference CPU path, OpenMP over the host cores) on the same workload.  After
 the timed steps it also times the commit's BLAKE3 column tree over the
-resident codewords (`commit_tree`, reported beside `value`, not in it).
+resident codewords (`commit_tree`) and the X4 extension-field transforms
+(`x4`: the rate-1/8 Fp2 encode NTT, codeword fold, Moebius inverse), each
+reported beside `value`, not in it.
 """
 from __future__ import annotations
 
@@ -186,6 +188,56 @@ def commit_tree(b, wl: Workload, reps: int = 10) -> dict:
             "achieved_gbs": round(matrix / ms / 1e6, 1), "reps": reps}
 
 
+def x4_transforms(b, log_n: int = 24, reps: int = 10) -> dict:
+    """The X4 extension-field transforms (not part of `value`): the rate-1/8
+    encode NTT of 2^(log_n - 3) Fp2 coefficients into 2^log_n points
+    (encode_rate_eighth, rust/volta-pcs/src/x4/ntt.rs:124-130), the fold of that
+    codeword (ntt.rs:238-256) and the Moebius inverse of 2^(log_n - 3) values,
+    each timed with the library's HIP events.  Algorithmic bytes: the NTT reads
+    the coefficients and writes the codeword once (16 B per element), the fold
+    reads n and writes n/2 elements, the Moebius reads and writes its table."""
+    import numpy as np
+    from volta_mi355x import FP2
+    n, m = 1 << log_n, 1 << (log_n - 3)
+    g = np.random.Generator(np.random.PCG64(33))
+    coeffs = b.upload_device(g.integers(0, 0xFFFF_FFFF_0000_0001, size=(m, 2), dtype=np.uint64), FP2)
+    arena = b.alloc_device(n + n // 2, FP2)
+    table = b.upload_device(g.integers(0, 0xFFFF_FFFF_0000_0001, size=(m, 2), dtype=np.uint64), FP2)
+    lib, raw = b.lib, b.raw
+
+    def timed(op, call):
+        for _ in range(2):
+            b._check(call())
+        b.synchronize()
+        b.reset_stats()
+        for _ in range(reps):
+            b._check(call())
+        b.synchronize()
+        s = b.get_stats()
+        return s["kernel_ns"][op] / max(s["calls"][op], 1) / 1e6
+
+    ntt_ms = timed("pcs_ntt", lambda: lib.volta_mi355x_x4_ntt_fp2_device(raw, coeffs.id, 0, m, n, arena.id, 0))
+    fold_ms = timed("pcs_rows", lambda: lib.volta_cuda_x4c_direct_fold_arena(raw, arena.id, 0, n, n * 16, 12345,
+                                                                             678))
+    mob_ms = timed("pcs_rows", lambda: lib.volta_cuda_fp2_mobius_inverse_inplace_device(raw, table.id, 0, m))
+    for x in (coeffs, arena, table):
+        b.free_device(x)
+    ntt_bytes, fold_bytes, mob_bytes = 16 * (m + n), 16 * (n + n // 2), 32 * m
+    passes = 1 if log_n <= 12 else 2 if log_n <= 20 else 3 if log_n <= 30 else 4
+    return {
+        "ntt": {"kernel": "volta_mi355x_x4_ntt_fp2_device (gather + column passes)", "coefficients": m,
+                "points": n, "passes": passes, "ms": round(ntt_ms, 4), "algorithmic_bytes": ntt_bytes,
+                "pass_bytes": 16 * m + 16 * n + (passes - 1) * 32 * n,
+                "achieved_gbs": round(ntt_bytes / ntt_ms / 1e6, 1)},
+        "fold": {"kernel": "volta_cuda_x4c_direct_fold_arena", "input_len": n, "ms": round(fold_ms, 4),
+                 "algorithmic_bytes": fold_bytes, "achieved_gbs": round(fold_bytes / fold_ms / 1e6, 1)},
+        "mobius_inverse": {"kernel": "volta_cuda_fp2_mobius_inverse_inplace_device", "n": m,
+                           "ms": round(mob_ms, 4), "algorithmic_bytes": mob_bytes,
+                           "achieved_gbs": round(mob_bytes / mob_ms / 1e6, 1)},
+        "reps": reps,
+    }
+
+
 def cpu_baseline(name: str, wl: Workload) -> dict:
     """The oracle's restatement of the reference CPU path (per-row radix-2 DIT
     NttPlan::forward + combine_rows), OpenMP over this host's cores."""
@@ -249,6 +301,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-copy-probe", action="store_true")
     ap.add_argument("--no-commit-tree", action="store_true")
+    ap.add_argument("--no-x4", action="store_true")
+    ap.add_argument("--x4-log-n", type=int, default=24)
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
@@ -283,6 +337,10 @@ def main() -> int:
     if not a.no_commit_tree and a.config != "c5":
         log("commit tree over the codewords")
         tree = commit_tree(b, wl)
+    x4 = None
+    if not a.no_x4:
+        log(f"X4 transforms at 2^{a.x4_log_n} points")
+        x4 = x4_transforms(b, a.x4_log_n)
     copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
     wl_close = wl.close
     cpu = None
@@ -322,6 +380,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "kernel_ms_per_step": {k: round(v / a.steps / 1e6, 4) for k, v in stats["kernel_ns"].items() if v},
         "commit_tree": tree,
+        "x4": x4,
     }
     print(json.dumps(out), flush=True)
     return 0

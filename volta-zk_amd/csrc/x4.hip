@@ -54,6 +54,21 @@ constexpr int THREADS = 256;
 constexpr int GBITS = 12;                       // inner table: w_4096^j, j < 2048
 constexpr int TILE_BITS = 12;                   // Fp2 per workgroup tile: 2^12 (64 KiB in LDS)
 constexpr int RUN_BITS = 2;                     // C = Q = 4 adjacent columns / rows per tile
+constexpr int PASS_BITS = TILE_BITS - RUN_BITS; // largest radix of a multi-pass transform
+constexpr bool XCD_SWIZZLE = false;             // consecutive tiles on one XCD (shared L2)
+static_assert(PASS_BITS <= GBITS, "the inner table covers radices up to 2^GBITS");
+
+// Tile index of this workgroup.  Workgroups are dispatched round-robin over
+// the 8 XCDs (blockIdx.x mod 8); with XCD_SWIZZLE the tiles an XCD runs back to
+// back are consecutive, so neighbouring tiles' shared cache lines meet in one L2.
+__device__ __forceinline__ uint64_t tile_id() {
+    const uint64_t b = blockIdx.x;
+    if constexpr (XCD_SWIZZLE) {
+        const uint64_t g = gridDim.x;
+        if ((g & 7) == 0) return (b & 7) * (g >> 3) + (b >> 3);
+    }
+    return b;
+}
 constexpr uint64_t ROOT33_C1 = 0x076de30b51a3f645ull;
 constexpr uint64_t INV2 = 0x7FFFFFFF80000001ull;  // (p + 1) / 2
 
@@ -108,8 +123,8 @@ struct Digits {
 // Gather pass: output row r (R = 2^rb elements) is the DFT of
 // x[nat(r) + 2^(nb - rb) j], j < R.  A workgroup takes the Q = 2^qb rows
 // r = (g Q + t) S + rest, t < Q (S = 2^mid_bits rows per value of i_1), whose
-// nat(r) = g Q + t + R_1 nat'(rest) are adjacent.  Reads at index >= len are
-// zero.
+// nat(r) = g Q + t + R_1 nat'(rest) are adjacent; tiles run g fastest, so
+// consecutive tiles read adjacent runs.  Reads at index >= len are zero.
 __global__ __launch_bounds__(THREADS) void gather_pass(const u64x2* __restrict__ x, uint64_t len,
                                                        u64x2* __restrict__ y, int nb, int rb, int qb, Digits d,
                                                        const uint64_t* inner) {
@@ -117,8 +132,10 @@ __global__ __launch_bounds__(THREADS) void gather_pass(const u64x2* __restrict__
     const uint32_t R = 1u << rb, Q = 1u << qb;
     const uint32_t QR = Q << rb;
     const int mid_bits = nb - rb - d.r1;
-    const uint64_t g = static_cast<uint64_t>(blockIdx.x) >> mid_bits;
-    const uint64_t rest = static_cast<uint64_t>(blockIdx.x) & ((uint64_t{1} << mid_bits) - 1);
+    const int gbits = d.r1 - qb;  // groups of Q first digits
+    const uint64_t blk = tile_id();
+    const uint64_t g = blk & ((uint64_t{1} << gbits) - 1);
+    const uint64_t rest = blk >> gbits;
     uint64_t natr = 0;
     int shift = mid_bits, scale = 0;
     for (int j = 0; j < d.count; ++j) {
@@ -155,8 +172,9 @@ __global__ __launch_bounds__(THREADS) void col_pass(u64x2* a, int nb, int hb, in
     const uint32_t C = 1u << cb;
     const uint32_t CR = C << rb;
     const uint64_t lblocks = (uint64_t{1} << lb) >> cb;
-    const uint64_t h = blockIdx.x / lblocks;
-    const uint64_t l0 = (blockIdx.x - h * lblocks) << cb;
+    const uint64_t blk = tile_id();
+    const uint64_t h = blk / lblocks;
+    const uint64_t l0 = (blk - h * lblocks) << cb;
     const uint64_t base = ((h << rb) << lb) + l0;
     for (uint32_t e = threadIdx.x; e < CR; e += THREADS) {
         const uint32_t i = e >> cb, c = e & (C - 1);
@@ -289,13 +307,22 @@ bool root33_consistent() {
 // Pass radices for a 2^nb-point transform: one pass up to 2^12, else 2, 3 or 4
 // passes of at most 2^10 (the last one, the gather, first in execution).
 int plan(int nb, int* r) {
-    if (nb <= x4::TILE_BITS) {
+    if (nb <= std::min(x4::TILE_BITS, x4::GBITS)) {
         r[0] = nb;
         return 1;
     }
-    const int passes = nb <= 20 ? 2 : nb <= 30 ? 3 : 4;
+    const int passes = (nb + x4::PASS_BITS - 1) / x4::PASS_BITS;
+    if (passes > 4) return 0;
     for (int p = 0; p < passes; ++p) r[p] = nb / passes + (p < nb % passes ? 1 : 0);
     return passes;
+}
+
+template <class K>
+int set_lds(Context* c, K kernel, size_t lds) {
+    if (lds <= 65536) return 0;
+    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    return 0;
 }
 
 }  // namespace
@@ -319,6 +346,7 @@ int x4_ntt(Context* c, const X4Tables& tb, const gl::Fp2* in, uint64_t len, gl::
     const int nb = tb.nb;
     int r[4] = {0, 0, 0, 0};
     const int passes = plan(nb, r);
+    if (passes == 0) return fail_msg(c, "X4 NTT size needs more than four passes");
     const auto* x = reinterpret_cast<const u64x2*>(in);
     auto* y = reinterpret_cast<u64x2*>(out);
     // gather: the last digit's DFT, rows in (i_1, .., i_(P-1)) order
@@ -332,7 +360,9 @@ int x4_ntt(Context* c, const X4Tables& tb, const gl::Fp2* in, uint64_t len, gl::
         d.bits[1] = r[2];
         const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
         const size_t lds = size_t{16} << (rb + qb);
-        if (blocks > 0x7FFFFFFFull || lds > 65536) return fail_msg(c, "X4 NTT pass exceeds its launch limits");
+        if (blocks > 0x7FFFFFFFull || lds > (size_t{16} << TILE_BITS))
+            return fail_msg(c, "X4 NTT pass exceeds its launch limits");
+        if (set_lds(c, gather_pass, lds)) return -1;
         hipLaunchKernelGGL(gather_pass, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds, c->stream, x, len, y,
                            nb, rb, qb, d, tb.inner);
         VMX_HIP(c, hipGetLastError());
@@ -344,7 +374,9 @@ int x4_ntt(Context* c, const X4Tables& tb, const gl::Fp2* in, uint64_t len, gl::
         const int cb = std::min(RUN_BITS, lb);
         const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
         const size_t lds = size_t{16} << (rb + cb);
-        if (blocks > 0x7FFFFFFFull || lds > 65536) return fail_msg(c, "X4 NTT pass exceeds its launch limits");
+        if (blocks > 0x7FFFFFFFull || lds > (size_t{16} << TILE_BITS))
+            return fail_msg(c, "X4 NTT pass exceeds its launch limits");
+        if (set_lds(c, col_pass, lds)) return -1;
         hipLaunchKernelGGL(col_pass, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds, c->stream, y, nb, hb, rb,
                            lb, cb, tb.inner, tb.split, tb.split_h);
         VMX_HIP(c, hipGetLastError());
@@ -387,6 +419,7 @@ int fp2_mobius(Context* c, gl::Fp2* values, uint64_t n, bool inverse) {
         const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
         const size_t lds = size_t{16} << (rb + cb);
         if (blocks > 0x7FFFFFFFull) return fail_msg(c, "Moebius pass exceeds its launch limits");
+        if (set_lds(c, mobius_pass, lds)) return -1;
         hipLaunchKernelGGL(mobius_pass, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds, c->stream, a, rb,
                            lb, cb, inverse ? 1 : 0);
         VMX_HIP(c, hipGetLastError());
