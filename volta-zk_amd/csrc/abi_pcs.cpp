@@ -40,9 +40,11 @@ int resident_ntt(Context* c, const uint64_t* in, size_t in_stride, size_t msg_le
                  uint64_t* out, bool inverse) {
     uint64_t h2d = 0;
     TwiddleSet* t = nullptr;
-    if (inverse ? ensure_inverse_twiddles(c, n, &h2d, &t) : ensure_twiddles(c, n, &h2d, &t)) return -1;
+    if (ensure_twiddles(c, n, &h2d, &t)) return -1;
+    // the pass engine (t->reg) computes the inverse from the forward tables
+    if (inverse && !t->reg && ensure_inverse_twiddles(c, n, &h2d, &t)) return -1;
     if (begin_op(c) || mark_op(c, 1)) return -1;
-    if (ntt_fp_rows(c, in, in_stride, msg_len, rows, n, out, inverse ? t->inv : t->fwd, inverse)) return -1;
+    if (ntt_fp_rows(c, in, in_stride, msg_len, rows, n, out, t, inverse)) return -1;
     if (mark_op(c, 2)) return -1;
     return finish_op(c, OP_PCS_NTT, h2d, 0);
 }
@@ -90,7 +92,7 @@ VMX_API int volta_cuda_ntt_fp2_batch_device(void* raw, uint64_t in_id, size_t in
         TwiddleSet* t = nullptr;
         if (ensure_twiddles(c, n, &h2d, &t)) return -1;
         if (begin_op(c) || mark_op(c, 1)) return -1;
-        if (ntt_fp2_rows(c, static_cast<const uint64_t*>(in), rows, n, static_cast<uint64_t*>(out), t->fwd))
+        if (ntt_fp2_rows(c, static_cast<const uint64_t*>(in), rows, n, static_cast<uint64_t*>(out), t))
             return -1;
         if (mark_op(c, 2)) return -1;
         return finish_op(c, OP_PCS_NTT, h2d, 0);
@@ -115,7 +117,7 @@ int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size
     if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<uint64_t>(c, WS_IN), msgs, in_bytes, hipMemcpyHostToDevice, c->stream));
     h2d += in_bytes;
     if (mark_op(c, 1)) return -1;
-    if (ntt_fp_rows(c, ws<uint64_t>(c, WS_IN), msg_len, msg_len, rows, n, ws<uint64_t>(c, WS_OUT), t->fwd, false))
+    if (ntt_fp_rows(c, ws<uint64_t>(c, WS_IN), msg_len, msg_len, rows, n, ws<uint64_t>(c, WS_OUT), t, false))
         return -1;
     if (mark_op(c, 2)) return -1;
     VMX_HIP(c, hipMemcpyAsync(out, ws<uint64_t>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
@@ -153,7 +155,7 @@ VMX_API int volta_cuda_ntt_fp2(void* raw, const Fp2* msg, size_t msg_len, size_t
         if (bytes > in_bytes && zero_bytes(c, ws<unsigned char>(c, WS_IN) + in_bytes, bytes - in_bytes)) return -1;
         h2d += bytes;
         if (mark_op(c, 1)) return -1;
-        if (ntt_fp2_rows(c, ws<uint64_t>(c, WS_IN), 1, n, ws<uint64_t>(c, WS_OUT), t->fwd)) return -1;
+        if (ntt_fp2_rows(c, ws<uint64_t>(c, WS_IN), 1, n, ws<uint64_t>(c, WS_OUT), t)) return -1;
         if (mark_op(c, 2)) return -1;
         VMX_HIP(c, hipMemcpyAsync(out, ws<Fp2>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
         return finish_op(c, OP_PCS_NTT, h2d, bytes);

@@ -200,6 +200,8 @@ int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out) {
         }
         if (upload_table(c, host, &t.fwd, h2d)) return -1;
     }
+    // the pass engine's tables come from fwd on the device: no further H2D
+    if (!t.reg && n <= (size_t{1} << 31) && reg_ntt_covers(n) && derive_reg_tables(c, &t)) return -1;
     *out = &t;
     return 0;
 }
@@ -704,6 +706,7 @@ VMX_API void volta_cuda_destroy(void* raw) {
             if (kv.second.inv) (void)hipFree(kv.second.inv);
             if (kv.second.grid) (void)hipFree(kv.second.grid);
             if (kv.second.split) (void)hipFree(kv.second.split);
+            if (kv.second.reg) (void)hipFree(kv.second.reg);
         }
         for (auto& p : c->pinned) {
             if (p.ready) (void)hipEventDestroy(p.ready);
@@ -902,7 +905,7 @@ VMX_API int volta_cuda_memory_breakdown(void* raw, uint64_t* workspace, uint64_t
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) w += half;
         if (kv.second.inv) w += half;
-        w += kv.second.grid_bytes + kv.second.split_bytes;
+        w += kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;
@@ -1275,7 +1278,7 @@ VMX_API int volta_cuda_x4c_control_state(void* raw, RawX4cControlState* out) {
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) r.workspace_device_bytes += half;
         if (kv.second.inv) r.workspace_device_bytes += half;
-        r.workspace_device_bytes += kv.second.grid_bytes + kv.second.split_bytes;
+        r.workspace_device_bytes += kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;

@@ -193,6 +193,11 @@ struct TwiddleSet {
     uint64_t* split = nullptr;
     size_t split_bytes = 0;
     int split_h = 0;
+    // The pass engine's tables (n >= 2^13), derived on the device from fwd:
+    // [w_4096^j, j < 2048][two-level table of w with h = reg_h].
+    uint64_t* reg = nullptr;
+    size_t reg_bytes = 0;
+    int reg_h = 0;
     size_t n = 0;
 };
 
@@ -265,6 +270,10 @@ T* ws(Context* c, int slot) {
 // bytes to *h2d (the reference's per-size upload, .cu:2675-2689).
 int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
 int ensure_inverse_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
+// Derives TwiddleSet::reg from t->fwd on the device (ntt_reg.hip); a no-op
+// when present.  ensure_twiddles calls it for every size the pass engine runs.
+int derive_reg_tables(Context* c, TwiddleSet* t);
+bool reg_ntt_covers(uint64_t n);
 // Two-level table of w^e for size n (TwiddleSet::split), uploaded once.
 int ensure_split_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out);
 // Device-built table of `bytes` for the fast encode, derived from t->fwd on

@@ -14,12 +14,14 @@ namespace vmx {
 
 int zero_bytes(Context* c, void* dst, size_t bytes);
 
-// rows x n forward (or inverse-scaled) NTT of u64 rows: input row r is
-// in[r*in_stride .. +msg_len), zero beyond; output rows are n wide.
+// rows x n forward (or inverse, n^-1 scaled) NTT of u64 rows: input row r is
+// in[r*in_stride .. +msg_len), zero beyond; output rows are n wide.  t is
+// ensure_twiddles(n)'s set; the inverse needs t->inv unless t->reg is present
+// (the pass engine, n >= 2^13).
 int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
-                uint64_t* out, const uint64_t* tw, bool inverse_scale_n);
+                uint64_t* out, const TwiddleSet* t, bool inverse);
 // Componentwise NTT of rows x n Fp2 (u64 pairs) with base-field twiddles.
-int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const uint64_t* tw);
+int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const TwiddleSet* t);
 // Fused PCS encode: messages lift(w) || pads || 0 transformed without
 // materialising the message rows.
 int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
@@ -59,6 +61,19 @@ int merkle_column_leaves(Context* c, const uint64_t* m, size_t rows, size_t cols
 int merkle_tree_levels(Context* c, uint32_t* tree, size_t leaves);
 int merkle_paths(Context* c, const uint32_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
                  uint32_t* paths);
+
+// Batched NTTs of 2^13 .. 2^33 points as passes of register four-steps
+// (ntt_reg.hip).  rows transforms of n = 2^nb elements of `planes` u64 (1: Fp,
+// 2: Fp2); input row r starts at in + r in_stride planes and holds len
+// elements (zero beyond), output rows are contiguous.  Roots are the X4 roots
+// (the base field's up to 2^31).  inverse: a_i = n^-1 sum_j A_j w^-ij (n <= 2^31).
+struct RegTables {
+    const uint64_t* inner = nullptr;  // w_4096^j, j < 2048
+    const uint64_t* split = nullptr;  // two-level table of b_min(nb,32)
+    int split_h = 0;
+};
+int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
+            uint64_t rows, int nb, int planes, bool inverse);
 
 // X4 extension-field transforms (x4.hip).  Tables for transforms and folds of
 // 2^nb points, nb in [1, 33]; uploaded once per size (adds to *h2d), so call

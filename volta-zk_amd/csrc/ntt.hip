@@ -4,7 +4,9 @@
 // out[j] = sum_i a_i w^(ij), w = 7^((p-1)/n), natural-order output.  Field sums
 // are exact, so any factorisation of the DFT gives bit-identical results.
 //
-// Generic paths (any power-of-two n):
+// u64 and Fp2 rows of n >= 2^13 run on the pass engine of ntt_reg.hip
+// (register four-steps with shift-only sub-DFTs).  The generic paths below
+// serve smaller rows and the i16 message loads (any power-of-two n):
 //   * n <= 2^14: one workgroup per row, the whole row in LDS (<= 128 KiB of the
 //     160 KiB per CU), bit-reversed load then radix-2^2 DIT passes (two stages
 //     per LDS round trip).  One HBM read + one HBM write per element.
@@ -240,15 +242,27 @@ static int run_ntt(Context* c, Load ld, Store st, size_t rows, size_t n, const u
     return 0;
 }
 
+static RegTables reg_tables(const TwiddleSet* t) {
+    RegTables rt;
+    rt.inner = t->reg;
+    rt.split = t->reg + 2048;
+    rt.split_h = t->reg_h;
+    return rt;
+}
+
 int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
-                uint64_t* out, const uint64_t* tw, bool inverse_scale_n) {
-    const uint64_t scale = inverse_scale_n ? gl::inv_host(gl::canon(n)) : 1;
+                uint64_t* out, const TwiddleSet* t, bool inverse) {
+    if (t->reg) return reg_ntt(c, reg_tables(t), in, in_stride, msg_len, out, rows, ilog2(n), 1, inverse);
+    const uint64_t scale = inverse ? gl::inv_host(gl::canon(n)) : 1;
+    const uint64_t* tw = inverse ? t->inv : t->fwd;
+    if (!tw) return fail_msg(c, "NTT twiddle table missing");
     return run_ntt(c, LoadU64{in, in_stride, msg_len}, StoreU64{out}, rows, n, tw, scale);
 }
 
-int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const uint64_t* tw) {
+int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const TwiddleSet* t) {
+    if (t->reg) return reg_ntt(c, reg_tables(t), in, n, n, out, rows, ilog2(n), 2, false);
     for (int comp = 0; comp < 2; ++comp)
-        if (run_ntt(c, LoadFp2Comp{in, n, comp}, StoreFp2Comp{out, comp}, rows, n, tw, 1)) return -1;
+        if (run_ntt(c, LoadFp2Comp{in, n, comp}, StoreFp2Comp{out, comp}, rows, n, t->fwd, 1)) return -1;
     return 0;
 }
 

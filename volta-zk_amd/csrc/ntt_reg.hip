@@ -1,0 +1,342 @@
+// ntt_reg.hip -- batched NTTs of 2^13 .. 2^33 points as passes over HBM,
+// each pass a register four-step; used by the base-field transforms
+// (ntt.hip: NttPlan::forward semantics, rust/volta-pcs/src/ntt.rs:34-70) and by
+// the X4 Fp2 transform (x4.hip, rust/volta-pcs/src/x4/ntt.rs:66-122).
+//
+// An n = 2^nb point transform, n = R_1 R_2 .. R_P with every R_p <= 2^8, runs in
+// P passes (decimation in time by the least significant input digit first):
+//   pass 1 ("gather"): row r = (i_1, .., i_(P-1)) (i_1 most significant) gets
+//     the R_P-point DFT of x[nat(r) + (n / R_P) j], j < R_P, with
+//     nat(r) = i_1 + R_1 (i_2 + R_2 (..)), stored contiguously as row r of
+//     the output.  A tile takes adjacent rows (adjacent i_1), so its reads are
+//     runs of 128 or 256 bytes.  Inputs at index >= len (the caller's zero
+//     tail) are read as zero and never stored.
+//   passes P-1 .. 1 ("columns"): the output is [H][R_p][L]
+//     (H = R_1 .. R_(p-1), L = R_(p+1) .. R_P); element (i, l) is multiplied by
+//     w(n)^(H i l) as it loads and column l gets the R_p-point DFT over i, in
+//     place.  A tile takes adjacent columns.
+// Each pass reads and writes every element once.  The roots are the X4 roots
+// (ntt_reg.hpp), which are the base field's for n <= 2^31.
+//
+// Each R = A B point DFT (A = 2^LA, B = 2^LB, both <= 16) is a four-step inside
+// the tile, with input index j = ja B + jb and output index k = ka + A kb:
+//   step 1: one thread takes the A inputs of one (coordinate, column, jb)
+//     straight from HBM into registers, DFTs them over ja with shift-only
+//     twiddles (every root of order <= 64 is a power of two), multiplies
+//     output ka by w_R^(jb ka) and parks them in LDS;
+//   step 2: one thread takes the B values of one (coordinate, column, ka),
+//     DFTs them over jb and stores Y[ka + A kb] straight to HBM.
+// LDS holds (coordinate, column) pairs fastest, then jb, then ka with a pitch
+// of PW (B + 1) words, so both steps' accesses avoid bank conflicts.
+//
+// Elements are PL u64 wide (PL = 1: Fp; PL = 2: Fp2, coordinate p of element e
+// at 2 e + p); each coordinate is transformed independently, except that the
+// imaginary twiddles of an X4 transform of 2^33 points mix them.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "context.hpp"
+#include "gl64.hpp"
+#include "gl64_shift.hpp"
+#include "kernels.hpp"
+#include "ntt_reg.hpp"
+
+namespace vmx {
+namespace nreg {
+
+// Exponent of the base root of order 2^L (L <= 6) as a power of two:
+// w_64 = 2^39, so w_(2^L) = 2^(39 2^(6-L)), exponents mod 192.
+template <int L>
+constexpr int ew_log() {
+    return (gl::E_W64 << (6 - L)) % 192;
+}
+
+// w_4096^e for e < 4096 from the inner table (w_4096^j, j < 2048; w_4096^2048 = -1).
+__device__ __forceinline__ uint64_t inner_pow(const uint64_t* inner, uint32_t e) {
+    return e < 2048 ? inner[e] : gl::neg(inner[e - 2048]);
+}
+
+// The partner lane's value (lane ^ 1): the other coordinate of the same element.
+__device__ __forceinline__ uint64_t partner(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v)), 1));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(v >> 32)), 1));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// Step 1's tail: v (natural order over ka after the A-point DFT) times
+// w_R^(jb ka), parked at (pc, jb, ka).
+template <int LA, int LB>
+__device__ __forceinline__ void park(uint64_t* s, const uint64_t* v, uint32_t pc, uint32_t jb, uint32_t PW,
+                                     uint32_t pitch, const uint64_t* inner) {
+    constexpr int A = 1 << LA, RB = LA + LB;
+    s[pc + PW * jb] = v[0];
+    gl::static_for<1, A>([&](auto ka_) {
+        constexpr int ka = decltype(ka_)::value;
+        s[pc + PW * jb + ka * pitch] = gl::mul32x4(v[ka], inner_pow(inner, (jb * ka) << (GBITS - RB)));
+    });
+}
+
+// Step 2's head: the B values of (pc, ka), DFT'd over jb (natural order over kb).
+template <int LB>
+__device__ __forceinline__ void unpark(const uint64_t* s, uint64_t* v, uint32_t pc, uint32_t ka, uint32_t PW,
+                                       uint32_t pitch) {
+    constexpr int B = 1 << LB;
+    gl::static_for<0, B>([&](auto jb_) {
+        constexpr int jb = decltype(jb_)::value;
+        v[gl::bitrev_c(jb, LB)] = s[pc + PW * jb + ka * pitch];
+    });
+    gl::dit_pow2<LB, ew_log<LB>()>(v);
+}
+
+// Gather pass of row blockIdx.y of a batch: tile of 2^qb rows.  Input row
+// `row` starts at x + row x_stride elements and holds len elements (zero
+// beyond); with reverse the transform reads x[(n - idx) mod n] (the inverse
+// transform as a forward one); every input is multiplied by scale unless it
+// is 1.  Output rows are n elements apart.
+template <int LA, int LB, int PL>
+__global__ __launch_bounds__(THREADS) void gather_reg(const uint64_t* __restrict__ x, uint64_t x_stride,
+                                                      uint64_t len, uint64_t* __restrict__ y, int nb, int qb,
+                                                      Digits d, const uint64_t* inner, int reverse, uint64_t scale) {
+    constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
+    extern __shared__ uint64_t s[];
+    x += blockIdx.y * x_stride * PL;
+    y += (static_cast<uint64_t>(blockIdx.y) << nb) * PL;
+    const int pwb = qb + (PL - 1);  // (coordinate, row) pairs: 2^pwb
+    const uint32_t PW = 1u << pwb;
+    const uint32_t pitch = PW * (B + 1);
+    uint64_t nat0, row0;
+    int mid_bits;
+    gather_tile(nb, RB, qb, d, nat0, row0, mid_bits);
+    const int sh = nb - RB;
+    const uint64_t nmask = (uint64_t{1} << nb) - 1;
+    for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
+        const uint32_t pc = job & (PW - 1), jb = job >> pwb;
+        const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
+        uint64_t v[A];
+        gl::static_for<0, A>([&](auto ja_) {
+            constexpr int ja = decltype(ja_)::value;
+            uint64_t idx = nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh);
+            if (reverse) idx = (uint64_t{0} - idx) & nmask;
+            uint64_t xv = idx < len ? x[PL * idx + plane] : 0;
+            if (scale != 1) xv = gl::mul32x4(xv, scale);
+            v[gl::bitrev_c(ja, LA)] = xv;
+        });
+        gl::dit_pow2<LA, ew_log<LA>()>(v);
+        park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
+    }
+    __syncthreads();
+    for (uint32_t job = threadIdx.x; job < (PW << LA); job += THREADS) {
+        const uint32_t pc = job & (PW - 1), ka = job >> pwb;
+        const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
+        uint64_t v[B];
+        unpark<LB>(s, v, pc, ka, PW, pitch);
+        const uint64_t out0 = ((row0 + (static_cast<uint64_t>(t) << mid_bits)) << RB) + ka;
+        gl::static_for<0, B>([&](auto kb_) {
+            constexpr int kb = decltype(kb_)::value;
+            y[PL * (out0 + A * kb) + plane] = v[kb];
+        });
+    }
+}
+
+// Column pass of row blockIdx.y of a batch, in place (rows n elements
+// apart).  The array is [H][R][L] (H = 2^hb, R = 2^(LA+LB), L = 2^lb,
+// n = 2^nb); the tile takes the 2^cb adjacent columns l0 .. of block h:
+// element (i, l) is multiplied by w(n)^(H i l) as it loads, then each column
+// gets the R-point DFT over i.  For an X4 transform of 2^33 points the last
+// pass (hb = 0) meets imaginary twiddles, which mix the two coordinates: each
+// lane then also reads its partner lane's coordinate.
+template <int LA, int LB, int PL>
+__global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, int lb, int cb, const uint64_t* inner,
+                                                   const uint64_t* split, int split_h) {
+    constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
+    extern __shared__ uint64_t s[];
+    a += (static_cast<uint64_t>(blockIdx.y) << nb) * PL;
+    const int pwb = cb + (PL - 1);
+    const uint32_t PW = 1u << pwb;
+    const uint32_t pitch = PW * (B + 1);
+    const uint64_t lblocks = (uint64_t{1} << lb) >> cb;
+    const uint64_t blk = tile_id();
+    const uint64_t h = blk / lblocks;
+    const uint64_t l0 = (blk - h * lblocks) << cb;
+    const uint64_t base = ((h << RB) << lb) + l0;
+    const bool mixed = PL == 2 && nb == 33 && hb == 0;  // uniform
+    for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
+        const uint32_t pc = job & (PW - 1), jb = job >> pwb;
+        const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
+        const uint64_t l = l0 + c;
+        uint64_t v[A];
+        gl::static_for<0, A>([&](auto ja_) {
+            constexpr int ja = decltype(ja_)::value;
+            const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+            const uint64_t xv = a[PL * (base + (i << lb) + c) + plane];
+            bool imag;
+            const uint64_t t = root_pow((i * l) << hb, nb, split, split_h, imag);
+            uint64_t r;
+            if constexpr (PL == 2) {
+                if (mixed) {
+                    const uint64_t other = partner(xv);
+                    // (v0 + v1 phi) (t phi) = 7 v1 t + v0 t phi
+                    r = !imag ? gl::mul32x4(xv, t)
+                              : plane == 0 ? mul7(gl::mul32x4(other, t)) : gl::mul32x4(other, t);
+                } else {
+                    r = gl::mul32x4(xv, t);
+                }
+            } else {
+                r = gl::mul32x4(xv, t);
+            }
+            v[gl::bitrev_c(ja, LA)] = r;
+        });
+        gl::dit_pow2<LA, ew_log<LA>()>(v);
+        park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
+    }
+    __syncthreads();
+    for (uint32_t job = threadIdx.x; job < (PW << LA); job += THREADS) {
+        const uint32_t pc = job & (PW - 1), ka = job >> pwb;
+        const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
+        uint64_t v[B];
+        unpark<LB>(s, v, pc, ka, PW, pitch);
+        gl::static_for<0, B>([&](auto kb_) {
+            constexpr int kb = decltype(kb_)::value;
+            a[PL * (base + ((static_cast<uint64_t>(ka) + A * kb) << lb) + c) + plane] = v[kb];
+        });
+    }
+}
+
+// Tables for the passes from the reference's table fwd = w^0 .. w^(n/2 - 1),
+// n = 2^nb >= 2^13: out = [w_4096^j, j < 2048][w^j, j < 2^h][w^(j 2^h), j < 2^(nb-h)].
+__global__ void derive_tables(const uint64_t* fwd, int nb, int h, uint64_t* out) {
+    const uint64_t half = uint64_t{1} << (nb - 1);
+    const uint64_t lo = uint64_t{1} << h, hi = uint64_t{1} << (nb - h);
+    const uint64_t total = 2048 + lo + hi;
+    for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < total;
+         j += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        uint64_t e;
+        if (j < 2048) e = j << (nb - GBITS);
+        else if (j < 2048 + lo) e = j - 2048;
+        else e = (j - 2048 - lo) << h;
+        out[j] = e < half ? fwd[e] : gl::neg(fwd[e - half]);
+    }
+}
+
+}  // namespace nreg
+
+namespace {
+
+using GatherFn = void (*)(const uint64_t*, uint64_t, uint64_t, uint64_t*, int, int, nreg::Digits, const uint64_t*, int,
+                          uint64_t);
+using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int);
+
+template <int PL>
+bool kernels_for(int rb, GatherFn* g, ColFn* col) {
+    switch (rb) {
+        case 5: *g = nreg::gather_reg<3, 2, PL>; *col = nreg::col_reg<3, 2, PL>; return true;
+        case 6: *g = nreg::gather_reg<3, 3, PL>; *col = nreg::col_reg<3, 3, PL>; return true;
+        case 7: *g = nreg::gather_reg<4, 3, PL>; *col = nreg::col_reg<4, 3, PL>; return true;
+        case 8: *g = nreg::gather_reg<4, 4, PL>; *col = nreg::col_reg<4, 4, PL>; return true;
+        default: return false;
+    }
+}
+
+// Pass radices: the fewest passes of at most 2^8, as even as possible.
+int plan(int nb, int* r) {
+    const int passes = (nb + nreg::PASS_BITS - 1) / nreg::PASS_BITS;
+    if (nb < nreg::MIN_BITS || passes > nreg::MAX_PASSES) return 0;
+    for (int p = 0; p < passes; ++p) r[p] = nb / passes + (p < nb % passes ? 1 : 0);
+    return passes;
+}
+
+// LDS bytes of a tile: 2^pwb (coordinate, column) pairs x A x (B + 1) words.
+size_t tile_lds(int rb, int pwb) {
+    const size_t A = size_t{1} << ((rb + 1) / 2), B = size_t{1} << (rb / 2);
+    return (size_t{1} << pwb) * A * (B + 1) * sizeof(uint64_t);
+}
+
+template <class K>
+int allow_lds(Context* c, K kernel, size_t lds) {
+    if (lds <= 65536) return 0;
+    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds)));
+    return 0;
+}
+
+}  // namespace
+
+bool reg_ntt_covers(uint64_t n) {
+    int r[nreg::MAX_PASSES];
+    int nb = 0;
+    while ((uint64_t{1} << nb) < n) ++nb;
+    return (uint64_t{1} << nb) == n && plan(nb, r) > 0;
+}
+
+int derive_reg_tables(Context* c, TwiddleSet* t) {
+    if (t->reg) return 0;
+    int nb = 0;
+    while ((size_t{1} << nb) < t->n) ++nb;
+    if (nb < nreg::MIN_BITS || nb > 31 || !t->fwd) return fail_msg(c, "pass tables need a size in [2^13, 2^31]");
+    const int h = (nb + 1) / 2;
+    const size_t words = 2048 + (size_t{1} << h) + (size_t{1} << (nb - h));
+    void* p = nullptr;
+    VMX_HIP(c, hipMalloc(&p, words * sizeof(uint64_t)));
+    ++c->stats.allocation_calls;
+    c->stats.live_device_bytes += words * sizeof(uint64_t);
+    c->stats.peak_device_bytes = std::max(c->stats.peak_device_bytes, c->stats.live_device_bytes);
+    t->reg = static_cast<uint64_t*>(p);
+    t->reg_bytes = words * sizeof(uint64_t);
+    t->reg_h = h;
+    hipLaunchKernelGGL(nreg::derive_tables, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256), 0, c->stream,
+                       static_cast<const uint64_t*>(t->fwd), nb, h, t->reg);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
+int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
+            uint64_t rows, int nb, int planes, bool inverse) {
+    int r[nreg::MAX_PASSES] = {};
+    const int passes = plan(nb, r);
+    if (passes == 0 || (planes != 1 && planes != 2)) return fail_msg(c, "NTT size outside the pass engine's range");
+    if (inverse && nb > 31) return fail_msg(c, "inverse transforms are defined up to 2^31 points");
+    const int wb = nreg::run_bits(nb, planes);
+    const uint64_t scale = inverse ? gl::inv_host(gl::canon(uint64_t{1} << nb)) : 1;
+    GatherFn g = nullptr;
+    ColFn col = nullptr;
+    auto pick = [&](int rb) { return planes == 1 ? kernels_for<1>(rb, &g, &col) : kernels_for<2>(rb, &g, &col); };
+    for (uint64_t r0 = 0; r0 < rows; r0 += 65535) {
+        const unsigned cnt = static_cast<unsigned>(std::min<uint64_t>(rows - r0, 65535));
+        const uint64_t* x = in + r0 * in_stride * planes;
+        uint64_t* y = out + (r0 << nb) * planes;
+        {  // gather: the last digit's DFT, rows in (i_1, .., i_(P-1)) order
+            const int rb = r[passes - 1];
+            const int qb = std::min(wb, r[0]);
+            nreg::Digits d{};
+            d.r1 = r[0];
+            d.count = passes - 2;
+            for (int j = 0; j < d.count; ++j) d.bits[j] = r[1 + j];
+            const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
+            const size_t lds = tile_lds(rb, qb + planes - 1);
+            if (!pick(rb) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+                return fail_msg(c, "NTT pass exceeds its launch limits");
+            if (allow_lds(c, g, lds)) return -1;
+            hipLaunchKernelGGL(g, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, x,
+                               in_stride, len, y, nb, qb, d, tb.inner, inverse ? 1 : 0, scale);
+            VMX_HIP(c, hipGetLastError());
+        }
+        int lbits = r[passes - 1];
+        for (int p = passes - 2; p >= 0; --p) {  // columns: digits P-1 .. 1, in place
+            const int rb = r[p], lb = lbits, hb = nb - rb - lb;
+            const int cb = std::min(wb, lb);
+            const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
+            const size_t lds = tile_lds(rb, cb + planes - 1);
+            if (!pick(rb) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+                return fail_msg(c, "NTT pass exceeds its launch limits");
+            if (allow_lds(c, col, lds)) return -1;
+            hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
+                               nb, hb, lb, cb, tb.inner, tb.split, tb.split_h);
+            VMX_HIP(c, hipGetLastError());
+            lbits += rb;
+        }
+    }
+    return 0;
+}
+
+}  // namespace vmx
