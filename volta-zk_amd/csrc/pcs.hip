@@ -286,10 +286,22 @@ static int launch_comb_groups(size_t combinations, F&& f) {
     return 0;
 }
 
+// Rows per partial: COMB_CHUNK, or fewer (down to 8) when the column blocks
+// times the chunks would not give about 1024 workgroups, so small matrices
+// still spread over the GPU's 256 CUs.  The reduce pass sums the chunks.
+static size_t comb_chunk(size_t rows, size_t col_blocks) {
+    size_t chunk = COMB_CHUNK;
+    while (chunk > 8 && col_blocks * ((rows + chunk - 1) / chunk) < 1024) chunk >>= 1;
+    return chunk;
+}
+
 int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
                      size_t cols, size_t pad, size_t combinations, Fp2* out) {
     const size_t msg_len = cols + pad;
-    const size_t chunks = (rows + COMB_CHUNK - 1) / COMB_CHUNK;
+    const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
+    const size_t col_blocks = (col_threads + COMB_THREADS - 1) / COMB_THREADS;
+    const size_t chunk = comb_chunk(rows, col_blocks);
+    const size_t chunks = (rows + chunk - 1) / chunk;
     size_t per_chunk = 0, bytes = 0, sum_bytes = 0;
     if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes) ||
         !mul_ok(chunks * combinations, 2 * sizeof(uint64_t), &sum_bytes))
@@ -300,22 +312,20 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
     Fp2* part = ws<Fp2>(c, WS_PARTIALS);
     uint64_t* sums = ws<uint64_t>(c, WS_AUX2);
     hipLaunchKernelGGL(coeff_chunk_sums, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(combinations)),
-                       dim3(256), 0, c->stream, coeffs, sums, rows, COMB_CHUNK);
+                       dim3(256), 0, c->stream, coeffs, sums, rows, chunk);
     VMX_HIP(c, hipGetLastError());
-    const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
-    const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
-                    static_cast<unsigned>(chunks));
+    const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
     // Vector row loads need a base and a row pitch aligned to COMB_COLS i16.
     const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * COMB_COLS) == 0) && (cols % COMB_COLS == 0);
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
                 hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
                                    static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
-                                   COMB_CHUNK, vec_ok);
+                                   chunk, vec_ok);
             else
                 hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
                                    static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
-                                   COMB_CHUNK, vec_ok);
+                                   chunk, vec_ok);
             VMX_HIP(c, hipGetLastError());
             return 0;
         }))
@@ -325,7 +335,7 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
                      static_cast<unsigned>(combinations));
         if (combinations > 65535) return fail_msg(c, "too many PCS combinations");
         hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs, part, rows, cols, pad,
-                           msg_len, combinations, COMB_CHUNK);
+                           msg_len, combinations, chunk);
         VMX_HIP(c, hipGetLastError());
     }
     hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
@@ -336,23 +346,24 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
 
 int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, const Fp2* coeffs,
                     size_t combinations, Fp2* out) {
-    const size_t chunks = (rows + COMB_CHUNK - 1) / COMB_CHUNK;
+    const size_t col_threads = (cols + FP_COLS - 1) / FP_COLS;
+    const size_t col_blocks = (col_threads + COMB_THREADS - 1) / COMB_THREADS;
+    const size_t chunk = comb_chunk(rows, col_blocks);
+    const size_t chunks = (rows + chunk - 1) / chunk;
     size_t per_chunk = 0, bytes = 0;
     if (!mul_ok(combinations, cols, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes))
         return fail_msg(c, "combination partials overflow size_t");
     if (chunks > 65535) return fail_msg(c, "combination row count exceeds the supported maximum");
     if (ensure_ws(c, WS_PARTIALS, bytes)) return -1;
     Fp2* part = ws<Fp2>(c, WS_PARTIALS);
-    const size_t col_threads = (cols + FP_COLS - 1) / FP_COLS;
-    const dim3 grid(static_cast<unsigned>((col_threads + COMB_THREADS - 1) / COMB_THREADS),
-                    static_cast<unsigned>(chunks));
+    const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
                 hipLaunchKernelGGL(combine_fp_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, m, coeffs, part,
-                                   rows, cols, c0, combinations, COMB_CHUNK);
+                                   rows, cols, c0, combinations, chunk);
             else
                 hipLaunchKernelGGL(combine_fp_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, m, coeffs, part,
-                                   rows, cols, c0, combinations, COMB_CHUNK);
+                                   rows, cols, c0, combinations, chunk);
             VMX_HIP(c, hipGetLastError());
             return 0;
         }))
