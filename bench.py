@@ -164,6 +164,35 @@ def copy_bandwidth(b, nbytes: int = 1 << 32, reps: int = 10) -> float:
     return 2 * nbytes / dt / 1e9
 
 
+def fp2_chain_peak(b, log_n: int = 20, rounds: int = 256, reps: int = 10) -> dict:
+    """Integer multiply peak from the reference's Fp2 chain kernel
+    (cuda/p7_goldilocks_roofline.cu:79-89: x = x*b + (j+1, 2j+3), `rounds`
+    times per element; its output checksum is pinned by the GPU tests), at the
+    reference's own configuration 2^20 x 256.  One Fp2 multiply counts as 5
+    base multiplies, the reference's convention (`fp_mul_per_fp2_mul`)."""
+    import numpy as np
+    from volta_mi355x import FP2
+    n = 1 << log_n
+    g = np.random.Generator(np.random.PCG64(5))
+    a = b.upload_device(g.integers(0, 0xFFFF_FFFF_0000_0001, size=(n, 2), dtype=np.uint64), FP2)
+    c = b.upload_device(g.integers(0, 0xFFFF_FFFF_0000_0001, size=(n, 2), dtype=np.uint64), FP2)
+    out = b.alloc_device(n, FP2)
+    L, r = b.lib, b.raw
+    b._check(L.volta_mi355x_probe_fp2_device(r, a.id, c.id, out.id, n, rounds))
+    b.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b._check(L.volta_mi355x_probe_fp2_device(r, a.id, c.id, out.id, n, rounds))
+    b.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    for x in (a, c, out):
+        b.free_device(x)
+    ops = n * rounds / dt
+    return {"probe": "Fp2 multiply-add chain (p7_goldilocks_roofline.cu:79-89)", "elements": n, "rounds": rounds,
+            "ms": round(dt * 1e3, 4), "fp2_mul_per_s": round(ops), "base_mul_equiv_per_s": round(5 * ops),
+            "reference_a100_fp2_mul_per_s": 41180802646.5}
+
+
 def commit_tree(b, wl: Workload, reps: int = 10) -> dict:
     """BLAKE3 column leaves + Merkle tree over the step's resident codeword
     matrix (the reference commit's last stage, ligero.rs:595-621), timed with
@@ -342,6 +371,7 @@ def main() -> int:
         log(f"X4 transforms at 2^{a.x4_log_n} points")
         x4 = x4_transforms(b, a.x4_log_n)
     copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
+    chain = None if a.no_copy_probe else fp2_chain_peak(b)
     wl_close = wl.close
     cpu = None
     if not a.no_cpu_baseline:
@@ -377,6 +407,7 @@ def main() -> int:
             "launches_per_step": launches_per_step,
             "hbm_copy_gbs": copy_gbs,
         },
+        "int_peak": chain,
         "cpu_baseline": cpu,
         "kernel_ms_per_step": {k: round(v / a.steps / 1e6, 4) for k, v in stats["kernel_ns"].items() if v},
         "commit_tree": tree,

@@ -308,8 +308,9 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
         return fail_msg(c, "PCS combination partials overflow size_t");
     if (chunks > 65535 || combinations > 65535)
         return fail_msg(c, "PCS combination row or combination count exceeds the supported maximum");
-    if (ensure_ws(c, WS_PARTIALS, bytes) || ensure_ws(c, WS_AUX2, sum_bytes)) return -1;
-    Fp2* part = ws<Fp2>(c, WS_PARTIALS);
+    // one chunk: the partials are the result, written straight into out
+    if ((chunks > 1 && ensure_ws(c, WS_PARTIALS, bytes)) || ensure_ws(c, WS_AUX2, sum_bytes)) return -1;
+    Fp2* part = chunks > 1 ? ws<Fp2>(c, WS_PARTIALS) : out;
     uint64_t* sums = ws<uint64_t>(c, WS_AUX2);
     hipLaunchKernelGGL(coeff_chunk_sums, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(combinations)),
                        dim3(256), 0, c->stream, coeffs, sums, rows, chunk);
@@ -338,6 +339,7 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
                            msg_len, combinations, chunk);
         VMX_HIP(c, hipGetLastError());
     }
+    if (chunks == 1) return 0;
     hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
                        dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
     VMX_HIP(c, hipGetLastError());
@@ -354,8 +356,8 @@ int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, con
     if (!mul_ok(combinations, cols, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes))
         return fail_msg(c, "combination partials overflow size_t");
     if (chunks > 65535) return fail_msg(c, "combination row count exceeds the supported maximum");
-    if (ensure_ws(c, WS_PARTIALS, bytes)) return -1;
-    Fp2* part = ws<Fp2>(c, WS_PARTIALS);
+    if (chunks > 1 && ensure_ws(c, WS_PARTIALS, bytes)) return -1;
+    Fp2* part = chunks > 1 ? ws<Fp2>(c, WS_PARTIALS) : out;  // one chunk: straight into out
     const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
@@ -368,6 +370,7 @@ int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, con
             return 0;
         }))
         return -1;
+    if (chunks == 1) return 0;
     hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
                        dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
     VMX_HIP(c, hipGetLastError());
