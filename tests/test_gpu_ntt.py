@@ -94,7 +94,7 @@ def test_ntt_offsets_and_input_preserved(backend, oracle):
 
 
 def test_inverse_round_trip_and_oracle(backend, oracle):
-    for bits, rows in [(6, 3), (13, 4), (16, 2)]:
+    for bits, rows in [(6, 3), (13, 4), (16, 2), (20, 1), (21, 1)]:
         n = 1 << bits
         host = rand_fp(200 + bits, (rows, n))
         inp = backend.upload_device(host.reshape(-1))
@@ -107,6 +107,21 @@ def test_inverse_round_trip_and_oracle(backend, oracle):
             backend.free_device(b)
         assert (back == host).all()
         assert (direct == oracle.ntt_inverse_batch(host)).all()
+
+
+def test_batch_beyond_one_launch_slice(backend, oracle):
+    """65,537 rows of 2^13: the pass engine launches at most 65,535 rows per
+    grid; rows on both sides of each slice boundary match the oracle."""
+    rows, n = 65537, 1 << 13
+    g = np.random.Generator(np.random.PCG64(65537))
+    host = g.integers(0, P, size=(rows, n), dtype=np.uint64)
+    inp = backend.upload_device(host.reshape(-1))
+    out = backend.ntt_fp_batch_device(inp, rows, n)
+    picks = [0, 1, 65533, 65534, 65535, 65536]
+    got = np.stack([backend.download_device(out, r * n, n) for r in picks])
+    backend.free_device(inp)
+    backend.free_device(out)
+    assert (got == oracle.ntt_forward_batch(host[picks].copy())).all()
 
 
 def test_host_entry_points(backend, oracle):
@@ -155,7 +170,11 @@ def test_compact_encode_device(backend, oracle):
                                                 (3, 4096, 0, 14), (2, 1024, 3, 15),
                                                 # the n = 2^13 fast path: full, partial and 1-column rows
                                                 (3, 1, 0, 13), (5, 1000, 0, 13), (64, 2047, 0, 13),
-                                                (1000, 2048, 0, 13)])
+                                                (1000, 2048, 0, 13),
+                                                # the reference's production layouts (layer_layout.rs:26-45):
+                                                # 2^13 or 2^15 columns + 512 pads -> 2^15 .. 2^18, fewer rows
+                                                (70, 2048, 512, 13), (3, 8192, 512, 15), (2, 8192, 512, 16),
+                                                (2, 32768, 512, 17), (1, 32768, 512, 18), (3, 5000, 37, 16)])
 def test_pcs_encode_fused_and_chain_match_oracle(backend, oracle, rows, cols, pad, bits):
     n = 1 << bits
     g = np.random.Generator(np.random.PCG64(rows * 1000 + cols))

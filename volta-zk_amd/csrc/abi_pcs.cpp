@@ -473,7 +473,7 @@ VMX_API int volta_mi355x_pcs_encode_device(void* raw, uint64_t w_id, size_t w_of
                                  t);
         if (rc < 0) return -1;
         if (rc == 1 && ntt_msg_i16_rows(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows,
-                                        cols, pad, code_len, static_cast<uint64_t*>(out), t->fwd))
+                                        cols, pad, code_len, static_cast<uint64_t*>(out), t))
             return -1;
         if (mark_op(c, 2)) return -1;
         return finish_op(c, OP_PCS_NTT, h2d, 0);

@@ -25,7 +25,7 @@ int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t
 // Fused PCS encode: messages lift(w) || pads || 0 transformed without
 // materialising the message rows.
 int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
-                     size_t n, uint64_t* out, const uint64_t* tw);
+                     size_t n, uint64_t* out, const TwiddleSet* t);
 // Fast path for the Ligero shapes (i16 messages with rate <= 1/2 and
 // n in [2^11, 2^14]); returns 1 when the shape is not covered.
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
@@ -74,6 +74,10 @@ struct RegTables {
 };
 int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
             uint64_t rows, int nb, int planes, bool inverse);
+// The same forward transform of Ligero message rows lift(w) || pads || 0
+// (cols i16 weights and pad u64 pads per row), without materialising them.
+int reg_ntt_msg_i16(Context* c, const RegTables& tb, const int16_t* w, const uint64_t* pads, uint64_t cols,
+                    uint64_t pad, uint64_t* out, uint64_t rows, int nb);
 
 // X4 extension-field transforms (x4.hip).  Tables for transforms and folds of
 // 2^nb points, nb in [1, 33]; uploaded once per size (adds to *h2d), so call

@@ -4,9 +4,9 @@
 // out[j] = sum_i a_i w^(ij), w = 7^((p-1)/n), natural-order output.  Field sums
 // are exact, so any factorisation of the DFT gives bit-identical results.
 //
-// u64 and Fp2 rows of n >= 2^13 run on the pass engine of ntt_reg.hip
-// (register four-steps with shift-only sub-DFTs).  The generic paths below
-// serve smaller rows and the i16 message loads (any power-of-two n):
+// Rows of n >= 2^13 (u64, Fp2, and i16 weights + pads message rows) run on the
+// pass engine of ntt_reg.hip (register four-steps with shift-only sub-DFTs).
+// The generic paths below serve smaller rows (any power-of-two n):
 //   * n <= 2^14: one workgroup per row, the whole row in LDS (<= 128 KiB of the
 //     160 KiB per CU), bit-reversed load then radix-2^2 DIT passes (two stages
 //     per LDS round trip).  One HBM read + one HBM write per element.
@@ -267,8 +267,9 @@ int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t
 }
 
 int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
-                     size_t n, uint64_t* out, const uint64_t* tw) {
-    return run_ntt(c, LoadMsgI16{w, pads, cols, pad}, StoreU64{out}, rows, n, tw, 1);
+                     size_t n, uint64_t* out, const TwiddleSet* t) {
+    if (t->reg) return reg_ntt_msg_i16(c, reg_tables(t), w, pads, cols, pad, out, rows, ilog2(n));
+    return run_ntt(c, LoadMsgI16{w, pads, cols, pad}, StoreU64{out}, rows, n, t->fwd, 1);
 }
 
 }  // namespace vmx

@@ -89,19 +89,46 @@ __device__ __forceinline__ void unpark(const uint64_t* s, uint64_t* v, uint32_t 
     gl::dit_pow2<LB, ew_log<LB>()>(v);
 }
 
-// Gather pass of row blockIdx.y of a batch: tile of 2^qb rows.  Input row
-// `row` starts at x + row x_stride elements and holds len elements (zero
-// beyond); with reverse the transform reads x[(n - idx) mod n] (the inverse
-// transform as a forward one); every input is multiplied by scale unless it
-// is 1.  Output rows are n elements apart.
-template <int LA, int LB, int PL>
-__global__ __launch_bounds__(THREADS) void gather_reg(const uint64_t* __restrict__ x, uint64_t x_stride,
-                                                      uint64_t len, uint64_t* __restrict__ y, int nb, int qb,
-                                                      Digits d, const uint64_t* inner, int reverse, uint64_t scale) {
+// Inputs of the gather pass.  Row `row` of a batch, element idx < n,
+// coordinate `plane`:
+// SrcU64: x + row x_stride elements of PL u64, len elements then zeros; with
+//   reverse the transform reads index (n - idx) mod n (the inverse transform
+//   as a forward one) and every input is multiplied by scale unless it is 1.
+struct SrcU64 {
+    const uint64_t* x;
+    uint64_t x_stride, len;
+    int reverse;
+    uint64_t scale;
+    __device__ __forceinline__ uint64_t load(uint64_t row, uint64_t idx, uint32_t plane, int PL, uint64_t nmask) const {
+        if (reverse) idx = (uint64_t{0} - idx) & nmask;
+        uint64_t v = idx < len ? x[(row * x_stride + idx) * PL + plane] : 0;
+        if (scale != 1) v = gl::mul32x4(v, scale);
+        return v;
+    }
+};
+// SrcMsgI16: the Ligero message row lift(w) || pads || 0 (reference
+//   pcs_messages_kernel, cuda/volta_cuda_backend.cu:2950-2958): cols i16
+//   weights lifted as signed residues, then pad u64 pads, then zeros.
+struct SrcMsgI16 {
+    const int16_t* w;
+    const uint64_t* pads;
+    uint64_t cols, pad;
+    __device__ __forceinline__ uint64_t load(uint64_t row, uint64_t idx, uint32_t, int, uint64_t) const {
+        if (idx < cols) return gl::from_i16(w[row * cols + idx]);
+        if (idx < cols + pad) return pads[row * pad + (idx - cols)];
+        return 0;
+    }
+};
+
+// Gather pass of row blockIdx.y of a batch: tile of 2^qb rows, inputs from
+// src, output rows n elements apart.
+template <int LA, int LB, int PL, class Src>
+__global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restrict__ y, int nb, int qb, Digits d,
+                                                      const uint64_t* inner) {
     constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
     extern __shared__ uint64_t s[];
-    x += blockIdx.y * x_stride * PL;
-    y += (static_cast<uint64_t>(blockIdx.y) << nb) * PL;
+    const uint64_t row = blockIdx.y;
+    y += (row << nb) * PL;
     const int pwb = qb + (PL - 1);  // (coordinate, row) pairs: 2^pwb
     const uint32_t PW = 1u << pwb;
     const uint32_t pitch = PW * (B + 1);
@@ -116,11 +143,8 @@ __global__ __launch_bounds__(THREADS) void gather_reg(const uint64_t* __restrict
         uint64_t v[A];
         gl::static_for<0, A>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
-            uint64_t idx = nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh);
-            if (reverse) idx = (uint64_t{0} - idx) & nmask;
-            uint64_t xv = idx < len ? x[PL * idx + plane] : 0;
-            if (scale != 1) xv = gl::mul32x4(xv, scale);
-            v[gl::bitrev_c(ja, LA)] = xv;
+            const uint64_t idx = nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh);
+            v[gl::bitrev_c(ja, LA)] = src.load(row, idx, plane, PL, nmask);
         });
         gl::dit_pow2<LA, ew_log<LA>()>(v);
         park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
@@ -223,17 +247,17 @@ __global__ void derive_tables(const uint64_t* fwd, int nb, int h, uint64_t* out)
 
 namespace {
 
-using GatherFn = void (*)(const uint64_t*, uint64_t, uint64_t, uint64_t*, int, int, nreg::Digits, const uint64_t*, int,
-                          uint64_t);
+template <class Src>
+using GatherFn = void (*)(Src, uint64_t*, int, int, nreg::Digits, const uint64_t*);
 using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int);
 
-template <int PL>
-bool kernels_for(int rb, GatherFn* g, ColFn* col) {
+template <int PL, class Src>
+bool kernels_for(int rb, GatherFn<Src>* g, ColFn* col) {
     switch (rb) {
-        case 5: *g = nreg::gather_reg<3, 2, PL>; *col = nreg::col_reg<3, 2, PL>; return true;
-        case 6: *g = nreg::gather_reg<3, 3, PL>; *col = nreg::col_reg<3, 3, PL>; return true;
-        case 7: *g = nreg::gather_reg<4, 3, PL>; *col = nreg::col_reg<4, 3, PL>; return true;
-        case 8: *g = nreg::gather_reg<4, 4, PL>; *col = nreg::col_reg<4, 4, PL>; return true;
+        case 5: *g = nreg::gather_reg<3, 2, PL, Src>; *col = nreg::col_reg<3, 2, PL>; return true;
+        case 6: *g = nreg::gather_reg<3, 3, PL, Src>; *col = nreg::col_reg<3, 3, PL>; return true;
+        case 7: *g = nreg::gather_reg<4, 3, PL, Src>; *col = nreg::col_reg<4, 3, PL>; return true;
+        case 8: *g = nreg::gather_reg<4, 4, PL, Src>; *col = nreg::col_reg<4, 4, PL>; return true;
         default: return false;
     }
 }
@@ -290,21 +314,20 @@ int derive_reg_tables(Context* c, TwiddleSet* t) {
     return 0;
 }
 
-int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
-            uint64_t rows, int nb, int planes, bool inverse) {
+// The passes of rows transforms with inputs from src; shift(src, r0) moves
+// src to row r0 for each launch slice of at most 65535 rows.
+template <int PL, class Src, class Shift>
+int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* out, uint64_t rows, int nb) {
     int r[nreg::MAX_PASSES] = {};
     const int passes = plan(nb, r);
-    if (passes == 0 || (planes != 1 && planes != 2)) return fail_msg(c, "NTT size outside the pass engine's range");
-    if (inverse && nb > 31) return fail_msg(c, "inverse transforms are defined up to 2^31 points");
-    const int wb = nreg::run_bits(nb, planes);
-    const uint64_t scale = inverse ? gl::inv_host(gl::canon(uint64_t{1} << nb)) : 1;
-    GatherFn g = nullptr;
+    if (passes == 0) return fail_msg(c, "NTT size outside the pass engine's range");
+    const int wb = nreg::run_bits(nb, PL);
+    GatherFn<Src> g = nullptr;
     ColFn col = nullptr;
-    auto pick = [&](int rb) { return planes == 1 ? kernels_for<1>(rb, &g, &col) : kernels_for<2>(rb, &g, &col); };
     for (uint64_t r0 = 0; r0 < rows; r0 += 65535) {
         const unsigned cnt = static_cast<unsigned>(std::min<uint64_t>(rows - r0, 65535));
-        const uint64_t* x = in + r0 * in_stride * planes;
-        uint64_t* y = out + (r0 << nb) * planes;
+        const Src s0 = shift(src, r0);
+        uint64_t* y = out + (r0 << nb) * PL;
         {  // gather: the last digit's DFT, rows in (i_1, .., i_(P-1)) order
             const int rb = r[passes - 1];
             const int qb = std::min(wb, r[0]);
@@ -313,12 +336,12 @@ int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_str
             d.count = passes - 2;
             for (int j = 0; j < d.count; ++j) d.bits[j] = r[1 + j];
             const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
-            const size_t lds = tile_lds(rb, qb + planes - 1);
-            if (!pick(rb) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            const size_t lds = tile_lds(rb, qb + PL - 1);
+            if (!kernels_for<PL, Src>(rb, &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, g, lds)) return -1;
-            hipLaunchKernelGGL(g, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, x,
-                               in_stride, len, y, nb, qb, d, tb.inner, inverse ? 1 : 0, scale);
+            hipLaunchKernelGGL(g, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, s0, y,
+                               nb, qb, d, tb.inner);
             VMX_HIP(c, hipGetLastError());
         }
         int lbits = r[passes - 1];
@@ -326,8 +349,8 @@ int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_str
             const int rb = r[p], lb = lbits, hb = nb - rb - lb;
             const int cb = std::min(wb, lb);
             const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
-            const size_t lds = tile_lds(rb, cb + planes - 1);
-            if (!pick(rb) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            const size_t lds = tile_lds(rb, cb + PL - 1);
+            if (!kernels_for<PL, Src>(rb, &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, col, lds)) return -1;
             hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
@@ -337,6 +360,35 @@ int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_str
         }
     }
     return 0;
+}
+
+int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
+            uint64_t rows, int nb, int planes, bool inverse) {
+    if (inverse && nb > 31) return fail_msg(c, "inverse transforms are defined up to 2^31 points");
+    const nreg::SrcU64 src{in, in_stride, len, inverse ? 1 : 0,
+                           inverse ? gl::inv_host(gl::canon(uint64_t{1} << nb)) : uint64_t{1}};
+    auto shift1 = [](nreg::SrcU64 s, uint64_t r0) {  // to the launch slice's first row
+        s.x += r0 * s.x_stride;
+        return s;
+    };
+    auto shift2 = [](nreg::SrcU64 s, uint64_t r0) {
+        s.x += r0 * s.x_stride * 2;
+        return s;
+    };
+    if (planes == 1) return run_passes<1>(c, tb, src, shift1, out, rows, nb);
+    if (planes == 2) return run_passes<2>(c, tb, src, shift2, out, rows, nb);
+    return fail_msg(c, "NTT elements are one or two u64");
+}
+
+int reg_ntt_msg_i16(Context* c, const RegTables& tb, const int16_t* w, const uint64_t* pads, uint64_t cols,
+                    uint64_t pad, uint64_t* out, uint64_t rows, int nb) {
+    const nreg::SrcMsgI16 src{w, pads, cols, pad};
+    auto shift = [](nreg::SrcMsgI16 s, uint64_t r0) {
+        s.w += r0 * s.cols;
+        if (s.pad) s.pads += r0 * s.pad;
+        return s;
+    };
+    return run_passes<1>(c, tb, src, shift, out, rows, nb);
 }
 
 }  // namespace vmx
