@@ -41,6 +41,10 @@ WORKLOADS = {
           "+ 2 challenge-power combinations",
     "c4": "c4: 2^15 x 2^12 packed-lane Fp -> 2^15 (rate 1/8)",
     "c5": "c5: 64 x 2^24 uniform Fp, forward + inverse NTT + 64-row combination + 256-column gather",
+    "p15": "p15: production layer layout 24,576 x 2^13 i16 + 512 device ChaCha8 pads -> 2^15 (rate 1/4): "
+           "pads + fused messages/encode (ligero.rs:468-511, layer_layout.rs:30)",
+    "p17": "p17: production layer layout 2,080 x 2^15 i16 + 512 device ChaCha8 pads -> 2^17 (rate 1/4): "
+           "pads + fused messages/encode (ligero.rs:468-511, layer_layout.rs:34)",
 }
 
 
@@ -90,6 +94,13 @@ class Workload:
             self.msgs = keep(b.upload_device(m.reshape(-1)))
             del m
             self.enc = keep(b.alloc_device(rows * n, np.uint64))
+        elif name in ("p15", "p17"):
+            w = W.gaussian_i16(f"volta-mi355x/{name}/weights", rows * cfg.msg_len)
+            self.w = keep(b.upload_device(w))
+            del w
+            self.pads = keep(b.alloc_device(rows * cfg.pad, np.uint64))
+            self.enc = keep(b.alloc_device(rows * n, np.uint64))
+            self.seed = (__import__("ctypes").c_uint8 * 32).from_buffer_copy(W.seed_bytes(f"volta-mi355x/{name}/pads"))
         elif name == "c5":
             x = W.c5_rows()
             self.msgs = keep(b.upload_device(x.reshape(-1)))
@@ -125,6 +136,12 @@ class Workload:
                                                            1, self.u.id, 0))
         elif self.name == "c4":
             self._ok(L.volta_mi355x_ntt_fp_encode_device(r, self.msgs.id, 0, rows, cfg.msg_len, n, self.enc.id, 0))
+        elif self.name in ("p15", "p17"):
+            # the resident commit's pads, then lift(w) || pads || 0 encoded in one launch
+            self._ok(L.volta_cuda_chacha8_prover_secret_fp_rows_device(r, self.pads.id, 0, self.seed, 0, rows,
+                                                                       cfg.pad))
+            self._ok(L.volta_mi355x_pcs_encode_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, cfg.pad, n,
+                                                      self.enc.id, 0))
         elif self.name == "c5":
             self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
             self._ok(L.volta_mi355x_ntt_fp_inverse_batch_device(r, self.enc.id, 0, rows, n, self.back.id, 0))

@@ -109,6 +109,21 @@ def test_inverse_round_trip_and_oracle(backend, oracle):
         assert (direct == oracle.ntt_inverse_batch(host)).all()
 
 
+def test_forward_and_inverse_2_25(backend, oracle):
+    """One 2^25 row: three passes of radix 2^9 (the largest plan of that radix)."""
+    n = 1 << 25
+    host = rand_fp(25, (1, n))
+    inp = backend.upload_device(host.reshape(-1))
+    fwd = backend.ntt_fp_batch_device(inp, 1, n)
+    inv = backend.ntt_fp_inverse_batch_device(fwd, 1, n)
+    got = backend.download_device(fwd).reshape(1, n)
+    back = backend.download_device(inv).reshape(1, n)
+    for b in (inp, fwd, inv):
+        backend.free_device(b)
+    assert (back == host).all()
+    assert (got == oracle.ntt_forward_batch(host)).all()
+
+
 def test_batch_beyond_one_launch_slice(backend, oracle):
     """65,537 rows of 2^13: the pass engine launches at most 65,535 rows per
     grid; rows on both sides of each slice boundary match the oracle."""

@@ -3,7 +3,8 @@
 // (ntt.hip: NttPlan::forward semantics, rust/volta-pcs/src/ntt.rs:34-70) and by
 // the X4 Fp2 transform (x4.hip, rust/volta-pcs/src/x4/ntt.rs:66-122).
 //
-// An n = 2^nb point transform, n = R_1 R_2 .. R_P with every R_p <= 2^8, runs in
+// An n = 2^nb point transform, n = R_1 R_2 .. R_P with every R_p <= 2^8 (2^9 for
+// one-plane rows below 2^26, ntt_reg.hpp: pass_bits), runs in
 // P passes (decimation in time by the least significant input digit first):
 //   pass 1 ("gather"): row r = (i_1, .., i_(P-1)) (i_1 most significant) gets
 //     the R_P-point DFT of x[nat(r) + (n / R_P) j], j < R_P, with
@@ -18,7 +19,7 @@
 // Each pass reads and writes every element once.  The roots are the X4 roots
 // (ntt_reg.hpp), which are the base field's for n <= 2^31.
 //
-// Each R = A B point DFT (A = 2^LA, B = 2^LB, both <= 16) is a four-step inside
+// Each R = A B point DFT (A = 2^LA <= 32, B = 2^LB <= 16) is a four-step inside
 // the tile, with input index j = ja B + jb and output index k = ka + A kb:
 //   step 1: one thread takes the A inputs of one (coordinate, column, jb)
 //     straight from HBM into registers, DFTs them over ja with shift-only
@@ -258,13 +259,21 @@ bool kernels_for(int rb, GatherFn<Src>* g, ColFn* col) {
         case 6: *g = nreg::gather_reg<3, 3, PL, Src>; *col = nreg::col_reg<3, 3, PL>; return true;
         case 7: *g = nreg::gather_reg<4, 3, PL, Src>; *col = nreg::col_reg<4, 3, PL>; return true;
         case 8: *g = nreg::gather_reg<4, 4, PL, Src>; *col = nreg::col_reg<4, 4, PL>; return true;
+        case 9:
+            if constexpr (PL == 1) {
+                *g = nreg::gather_reg<5, 4, PL, Src>;
+                *col = nreg::col_reg<5, 4, PL>;
+                return true;
+            }
+            return false;
         default: return false;
     }
 }
 
-// Pass radices: the fewest passes of at most 2^8, as even as possible.
-int plan(int nb, int* r) {
-    const int passes = (nb + nreg::PASS_BITS - 1) / nreg::PASS_BITS;
+// Pass radices: the fewest passes of at most 2^pass_bits, as even as possible.
+int plan(int nb, int planes, int* r) {
+    const int pb = nreg::pass_bits(nb, planes);
+    const int passes = (nb + pb - 1) / pb;
     if (nb < nreg::MIN_BITS || passes > nreg::MAX_PASSES) return 0;
     for (int p = 0; p < passes; ++p) r[p] = nb / passes + (p < nb % passes ? 1 : 0);
     return passes;
@@ -290,7 +299,7 @@ bool reg_ntt_covers(uint64_t n) {
     int r[nreg::MAX_PASSES];
     int nb = 0;
     while ((uint64_t{1} << nb) < n) ++nb;
-    return (uint64_t{1} << nb) == n && plan(nb, r) > 0;
+    return (uint64_t{1} << nb) == n && plan(nb, 1, r) > 0;
 }
 
 int derive_reg_tables(Context* c, TwiddleSet* t) {
@@ -319,7 +328,7 @@ int derive_reg_tables(Context* c, TwiddleSet* t) {
 template <int PL, class Src, class Shift>
 int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* out, uint64_t rows, int nb) {
     int r[nreg::MAX_PASSES] = {};
-    const int passes = plan(nb, r);
+    const int passes = plan(nb, PL, r);
     if (passes == 0) return fail_msg(c, "NTT size outside the pass engine's range");
     const int wb = nreg::run_bits(nb, PL);
     GatherFn<Src> g = nullptr;

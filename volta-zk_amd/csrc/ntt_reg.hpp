@@ -18,7 +18,7 @@ namespace nreg {
 
 constexpr int THREADS = 256;
 constexpr int GBITS = 12;          // inner table: w_4096^j, j < 2048
-constexpr int PASS_BITS = 8;       // largest radix of one pass
+constexpr int PASS_BITS = 8;       // largest radix of one pass (2^9: see pass_bits)
 constexpr int MIN_BITS = 13;       // smallest transform run as passes (below: one LDS tile)
 constexpr int MAX_PASSES = 5;      // 2^33 = five passes of at most 2^8
 constexpr bool XCD_SWIZZLE = false;  // consecutive tiles on one XCD (shared L2)
@@ -32,6 +32,13 @@ static_assert(PASS_BITS <= GBITS, "the inner table covers radices up to 2^GBITS"
 __host__ __device__ constexpr int run_bits(int nb, int planes) {
     return (nb >= 26 ? 4 : 3) + (planes == 1 ? 1 : 0);
 }
+
+// Largest radix of a pass for elements of `planes` u64: 2^9 for one-plane
+// rows below 2^26 points, whose radix-2^9 tiles stay at 70 KB of LDS (two per
+// CU); that saves a pass at 2^17, 2^18 and 2^25 (measured: 2^17 rows 4.4 ms
+// against 5.4 ms in three passes).  2^8 otherwise: a radix-2^9 tile of Fp2 or
+// of 32 adjacent rows needs 139 KB, one per CU, and ran 1.8x slower.
+__host__ __device__ constexpr int pass_bits(int nb, int planes) { return planes == 1 && nb < 26 ? 9 : PASS_BITS; }
 
 // Tile index of this workgroup.  Workgroups are dispatched round-robin over
 // the 8 XCDs (blockIdx.x mod 8); with XCD_SWIZZLE the tiles an XCD runs back to

@@ -16,6 +16,13 @@ C4  2^15 x 2^12 Fp, each four uniform i16 lanes as a little-endian base-2^16
     integer canonicalised with Fp::new -> 2^15 (rate 1/8).
 C5  64 x 2^24 uniform Fp, forward then inverse NTT, a 64-row combination,
     and a gather of 256 seeded columns.
+
+Two further configurations follow the reference's production layer layouts
+(rust/volta-pcs/src/layer_layout.rs:30, 34) and its resident commit chain
+(ligero.rs:468-511): i16 weights ~ N(0, 2000^2) plus 512 ChaCha8 masking pads
+per row, generated on the device each commit, encoded as lift(w) || pads || 0.
+P15 24,576 x 2^13 i16 + 512 pads -> 2^15.
+P17 2,080 x 2^15 i16 + 512 pads -> 2^17.
 """
 from __future__ import annotations
 
@@ -49,6 +56,7 @@ class Config:
     n: int           # codeword length
     kind: str        # "fp" (u64 messages) or "i16"
     combinations: int
+    pad: int = 0     # ChaCha8 pads per row after the i16 weights
 
     @property
     def elements(self) -> int:
@@ -56,8 +64,9 @@ class Config:
 
     @property
     def algorithmic_bytes(self) -> int:
-        """Input read once + codewords written once."""
-        return self.rows * self.msg_len * (8 if self.kind == "fp" else 2) + self.rows * self.n * 8
+        """Input read once + codewords written once (+ the pads written and read once)."""
+        return (self.rows * self.msg_len * (8 if self.kind == "fp" else 2) + self.rows * self.n * 8
+                + 2 * self.rows * self.pad * 8)
 
 
 CONFIGS = {
@@ -66,6 +75,8 @@ CONFIGS = {
     "c3": Config("c3", 1 << 16, 1 << 11, 1 << 13, "i16", 2),
     "c4": Config("c4", 1 << 15, 1 << 12, 1 << 15, "fp", 0),
     "c5": Config("c5", 64, 1 << 24, 1 << 24, "fp", 1),
+    "p15": Config("p15", 24576, 1 << 13, 1 << 15, "i16", 0, 512),
+    "p17": Config("p17", 2080, 1 << 15, 1 << 17, "i16", 0, 512),
 }
 
 SEED_C1_ROWS = seed_bytes("volta-mi355x/c1/rows")
