@@ -261,10 +261,10 @@ int volta_cuda_x4b_context_probe(void* ctx, const uint8_t* a1, size_t a2, uint8_
 int volta_cuda_x4b_n4_inner_tile(void* ctx, const VoltaFp2* a1, size_t a2, size_t a3, const uint16_t* a4, const uint8_t* a5, size_t a6, uint64_t a7, uint32_t a8, uint8_t a9, uint8_t a10, uint8_t* a11);
 /* rust/volta-accel/src/cuda.rs:694 (type X4bN4OuterNodes), loaded at cuda.rs:1351; out of scope here: returns -1 with a last_error message. */
 int volta_cuda_x4b_n4_outer_nodes(void* ctx, const uint8_t* a1, size_t a2, uint64_t a3, uint32_t a4, uint8_t a5, uint8_t a6, uint8_t a7, uint8_t* a8);
-/* rust/volta-accel/src/cuda.rs:696 (type X4cDirectFoldPinnedTile), loaded at cuda.rs:1353; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_x4c_direct_fold_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, size_t a7, size_t a8, uint64_t a9, uint64_t a10);
-/* rust/volta-accel/src/cuda.rs:709 (type X4cUploadPinned), loaded at cuda.rs:1355; out of scope here: returns -1 with a last_error message. */
-int volta_cuda_x4c_upload_pinned(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5);
+/* rust/volta-accel/src/cuda.rs:696 (type X4cDirectFoldPinnedTile), loaded at cuda.rs:1353; MI355X implementation. */
+int volta_cuda_x4c_direct_fold_pinned_tile(void* ctx, uint64_t pinned_id, size_t pinned_offset_bytes, uint64_t arena_id, size_t output_offset_bytes, size_t scratch_offset_bytes, size_t input_len, size_t output_start, size_t output_count, uint64_t challenge_c0, uint64_t challenge_c1);
+/* rust/volta-accel/src/cuda.rs:709 (type X4cUploadPinned), loaded at cuda.rs:1355; MI355X implementation. */
+int volta_cuda_x4c_upload_pinned(void* ctx, uint64_t pinned_id, size_t pinned_offset_bytes, uint64_t arena_id, size_t arena_offset_bytes, size_t bytes);
 /* rust/volta-accel/src/cuda.rs:710 (type X4cDirectFoldArena), loaded at cuda.rs:1357; MI355X implementation. */
 int volta_cuda_x4c_direct_fold_arena(void* ctx, uint64_t arena_id, size_t input_offset_bytes, size_t input_len, size_t output_offset_bytes, uint64_t challenge_c0, uint64_t challenge_c1);
 /* rust/volta-accel/src/cuda.rs:712 (type X4cActivationAddPinnedTile), loaded at cuda.rs:1360; out of scope here: returns -1 with a last_error message. */

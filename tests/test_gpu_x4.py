@@ -205,6 +205,66 @@ def test_x4_fold_of_encode_is_encode_of_fold(backend, oracle, bits, length):
         backend.free_device(arena)
 
 
+def test_x4_fold_pinned_tiles_match_oracle(backend, oracle):
+    """A codeword folded tile by tile from pinned host memory
+    (volta_cuda_x4c_direct_fold_pinned_tile) equals the whole fold; pinned
+    uploads land byte-exact (volta_cuda_x4c_upload_pinned)."""
+    from volta_mi355x import FP2
+    bits, tile = 14, 1000  # tiles of 1000 outputs, the last one short
+    n, half = 1 << bits, 1 << (bits - 1)
+    v = rand_fp2(77, n)
+    ch = tuple(int(c) for c in rand_fp2(78, 1)[0])
+    want = oracle.x4_fold_codeword(v, ch)
+    out_off, scratch_off = 0, half * 16
+    arena = backend.alloc_device(half + 2 * tile, FP2)
+    pin = backend.pinned_alloc(2 * tile * 16 * 2)  # two tile slots, used alternately
+    launches0 = backend.get_stats()["x4c_kernel_launches"]
+    try:
+        for k, start in enumerate(range(0, half, tile)):
+            cnt = min(tile, half - start)
+            slot = (k % 2) * 2 * tile * 16
+            backend.pinned_write(pin, slot, np.concatenate([v[start:start + cnt], v[half + start:half + start + cnt]]))
+            backend.x4c_direct_fold_pinned_tile(pin, slot, arena, out_off, scratch_off, n, start, cnt, ch)
+        got = backend.download_device(arena, 0, half).view(np.uint64).reshape(half, 2)
+        assert np.array_equal(got, want)
+        assert backend.get_stats()["x4c_kernel_launches"] - launches0 == -(-half // tile)
+        # the plain pinned upload
+        backend.pinned_write(pin, 0, v[:tile])
+        backend.x4c_upload_pinned(pin, 0, arena, scratch_off, tile * 16)
+        back = backend.download_device(arena, half, tile).view(np.uint64).reshape(tile, 2)
+        assert np.array_equal(back, v[:tile])
+    finally:
+        backend.pinned_wait_ready(pin)
+        backend.pinned_free(pin)
+        backend.free_device(arena)
+
+
+def test_x4_fold_pinned_tile_errors(backend):
+    from volta_mi355x import FP2
+    lib, raw = backend.lib, backend.raw
+    arena = backend.alloc_device(64, FP2)
+    pin = backend.pinned_alloc(1024)
+    f = lib.volta_cuda_x4c_direct_fold_pinned_tile
+    try:
+        assert f(raw, pin, 0, arena.id, 0, 512, 64, 0, 0, 1, 1) != 0  # no outputs
+        assert "invalid X4c pinned direct-fold geometry" in backend.last_error()
+        assert f(raw, pin, 0, arena.id, 0, 512, 64, 30, 3, 1, 1) != 0  # past n/2
+        assert "invalid X4c pinned direct-fold geometry" in backend.last_error()
+        assert f(raw, pin, 8, arena.id, 0, 512, 64, 0, 4, 1, 1) != 0
+        assert "misaligned" in backend.last_error()
+        assert f(raw, pin, 0, arena.id, 0, 256, 64, 0, 4, 1, 1) != 0  # scratch inside the output
+        assert "overlap" in backend.last_error()
+        assert f(raw, pin, 0, arena.id, 0, 512, 128, 0, 33, 1, 1) != 0  # 1056-byte tile, 1024-byte buffer
+        assert "out of bounds" in backend.last_error()
+        assert lib.volta_cuda_x4c_upload_pinned(raw, pin, 1000, arena.id, 0, 100) != 0
+        assert "out of bounds" in backend.last_error()
+        assert lib.volta_cuda_x4c_upload_pinned(raw, 12345, 0, arena.id, 0, 16) != 0
+        assert "pinned buffer id" in backend.last_error()
+    finally:
+        backend.pinned_free(pin)
+        backend.free_device(arena)
+
+
 # ---- Moebius inverse --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("bits,off", [(0, 0), (1, 0), (2, 1), (5, 0), (11, 3), (12, 0), (13, 0), (14, 2), (17, 0),

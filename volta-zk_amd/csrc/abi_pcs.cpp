@@ -8,6 +8,7 @@
 // single HIP stream; only entry points that return host data synchronise.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstring>
 #include <vector>
 
@@ -833,8 +834,94 @@ VMX_API int volta_cuda_x4c_direct_fold_arena(void* raw, uint64_t arena_id, size_
         const Fp2* pos = static_cast<const Fp2*>(in);
         if (x4_fold(c, tb, pos, pos + half, static_cast<Fp2*>(out), 0, half, Fp2{challenge_c0, challenge_c1}))
             return -1;
+        ++c->stats.x4c_kernel_launches;
         if (mark_op(c, 2)) return -1;
         return finish_op(c, OP_PCS_ROWS, h2d, 0, 0, 0, out_bytes);
+    });
+}
+
+// Replaces volta_cuda_x4c_upload_pinned (.cu:5808-5837): bytes from a pinned
+// host region to a resident region.  The pinned source is in flight until the
+// copy completes; another pinned upload from it is refused meanwhile.
+VMX_API int volta_cuda_x4c_upload_pinned(void* raw, uint64_t pinned_id, size_t pinned_offset_bytes, uint64_t arena_id,
+                                         size_t arena_offset_bytes, size_t bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !bytes) return fail_msg(c, "invalid X4c pinned upload");
+    return guarded(c, "X4c pinned upload", [&] {
+        void *src = nullptr, *dst = nullptr;
+        Pinned* owner = nullptr;
+        if (pinned_region(c, pinned_id, pinned_offset_bytes, bytes, &src, &owner) ||
+            region(c, arena_id, arena_offset_bytes, bytes, &dst))
+            return -1;
+        bool ready = false;
+        if (pinned_ready(c, owner, &ready)) return -1;
+        if (!ready) return reject(c, "X4c pinned upload source is still in flight");
+        if (begin_transfer(c)) return -1;
+        const auto t0 = std::chrono::steady_clock::now();
+        const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (e != hipSuccess) return fail_hip(c, "hipMemcpyAsync(X4c pinned upload)", e);
+        if (pinned_mark_in_flight(c, owner)) return -1;
+        ++c->stats.resident_h2d_host_calls;
+        c->stats.resident_h2d_host_call_ns += std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        return finish_transfer(c, bytes, true);
+    });
+}
+
+// Replaces volta_cuda_x4c_direct_fold_pinned_tile (.cu:5839-5923): outputs
+// output_start .. output_start + output_count of the fold of an input_len
+// codeword whose needed halves sit in a pinned tile (output_count positive
+// values v[j], then output_count negative values v[j + input_len/2]).  The
+// tile is staged through scratch (tile bytes at scratch_offset_bytes of the
+// arena) and the outputs land at output_offset_bytes + 16 output_start.
+VMX_API int volta_cuda_x4c_direct_fold_pinned_tile(void* raw, uint64_t pinned_id, size_t pinned_offset_bytes,
+                                                   uint64_t arena_id, size_t output_offset_bytes,
+                                                   size_t scratch_offset_bytes, size_t input_len, size_t output_start,
+                                                   size_t output_count, uint64_t challenge_c0,
+                                                   uint64_t challenge_c1) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !x4_fold_geometry(input_len, challenge_c0, challenge_c1) || !output_count ||
+        output_start > input_len / 2 || output_count > input_len / 2 - output_start)
+        return fail_msg(c, "invalid X4c pinned direct-fold geometry");
+    return guarded(c, "X4c pinned direct fold", [&] {
+        size_t tile_elems = 0, tile_bytes = 0, start_bytes = 0, tile_out_bytes = 0, out_bytes = 0;
+        if (!mul_ok(output_count, 2, &tile_elems) || !mul_ok(tile_elems, sizeof(Fp2), &tile_bytes) ||
+            !mul_ok(output_start, sizeof(Fp2), &start_bytes) || !mul_ok(output_count, sizeof(Fp2), &tile_out_bytes) ||
+            !mul_ok(input_len / 2, sizeof(Fp2), &out_bytes))
+            return fail_msg(c, "X4c pinned direct-fold byte geometry overflows size_t");
+        if ((pinned_offset_bytes | output_offset_bytes | scratch_offset_bytes) % 16 != 0)
+            return fail_msg(c, "misaligned X4c pinned direct-fold region");
+        void *src = nullptr, *scratch = nullptr, *out = nullptr;
+        Pinned* owner = nullptr;
+        if (pinned_region(c, pinned_id, pinned_offset_bytes, tile_bytes, &src, &owner) ||
+            region(c, arena_id, scratch_offset_bytes, tile_bytes, &scratch) ||
+            region(c, arena_id, output_offset_bytes, out_bytes, &out))
+            return -1;
+        if (scratch_offset_bytes < output_offset_bytes + out_bytes &&
+            output_offset_bytes < scratch_offset_bytes + tile_bytes)
+            return fail_msg(c, "X4c pinned direct-fold scratch/output overlap");
+        bool ready = false;
+        if (pinned_ready(c, owner, &ready)) return -1;
+        if (!ready) return reject(c, "X4c direct-fold pinned tile is still in flight");
+        uint64_t h2d = 0;
+        X4Tables tb;
+        if (x4_tables(c, log2_of(input_len), &h2d, &tb)) return -1;
+        if (begin_op(c)) return -1;
+        const auto t0 = std::chrono::steady_clock::now();
+        const hipError_t e = hipMemcpyAsync(scratch, src, tile_bytes, hipMemcpyHostToDevice, c->stream);
+        const auto t1 = std::chrono::steady_clock::now();
+        if (e != hipSuccess) return fail_hip(c, "hipMemcpyAsync(X4c direct-fold tile)", e);
+        if (pinned_mark_in_flight(c, owner)) return -1;
+        ++c->stats.resident_h2d_host_calls;
+        c->stats.resident_h2d_host_call_ns += std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+        if (mark_op(c, 1)) return -1;
+        const Fp2* pos = static_cast<const Fp2*>(scratch);
+        Fp2* dst = reinterpret_cast<Fp2*>(static_cast<unsigned char*>(out) + start_bytes);
+        if (x4_fold(c, tb, pos, pos + output_count, dst, output_start, output_count, Fp2{challenge_c0, challenge_c1}))
+            return -1;
+        ++c->stats.x4c_kernel_launches;
+        if (mark_op(c, 2)) return -1;
+        return finish_op(c, OP_PCS_ROWS, h2d + tile_bytes, 0, 0, 0, tile_out_bytes);
     });
 }
 

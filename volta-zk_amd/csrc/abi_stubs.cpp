@@ -220,14 +220,6 @@ VMX_API int volta_cuda_x4b_n4_outer_nodes(void* ctx, const uint8_t* a1, size_t a
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8; return vmx_out_of_scope(ctx, "volta_cuda_x4b_n4_outer_nodes");
 }
 
-VMX_API int volta_cuda_x4c_direct_fold_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, size_t a7, size_t a8, uint64_t a9, uint64_t a10) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8, (void)a9, (void)a10; return vmx_out_of_scope(ctx, "volta_cuda_x4c_direct_fold_pinned_tile");
-}
-
-VMX_API int volta_cuda_x4c_upload_pinned(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5) {
-    (void)a1, (void)a2, (void)a3, (void)a4, (void)a5; return vmx_out_of_scope(ctx, "volta_cuda_x4c_upload_pinned");
-}
-
 VMX_API int volta_cuda_x4c_activation_add_pinned_tile(void* ctx, uint64_t a1, size_t a2, uint64_t a3, size_t a4, size_t a5, size_t a6, uint64_t a7, uint64_t a8) {
     (void)a1, (void)a2, (void)a3, (void)a4, (void)a5, (void)a6, (void)a7, (void)a8; return vmx_out_of_scope(ctx, "volta_cuda_x4c_activation_add_pinned_tile");
 }

@@ -640,6 +640,41 @@ static Pinned* find_pinned(Context* c, uint64_t id) {
     return (p.active && p.generation == gen) ? &p : nullptr;
 }
 
+int pinned_region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out, Pinned** owner) {
+    Pinned* p = find_pinned(c, id);
+    if (!p) return fail_msg(c, "unknown or stale pinned buffer id");
+    if (offset_bytes > p->logical || bytes > p->logical - offset_bytes)
+        return fail_msg(c, "pinned buffer region is out of bounds");
+    *out = static_cast<unsigned char*>(p->ptr) + offset_bytes;
+    if (owner) *owner = p;
+    return 0;
+}
+
+int pinned_ready(Context* c, Pinned* p, bool* ready) {
+    if (!p->in_flight) {
+        *ready = true;
+        return 0;
+    }
+    const hipError_t e = hipEventQuery(p->ready);
+    if (e == hipSuccess) {
+        p->in_flight = false;
+        *ready = true;
+        return 0;
+    }
+    if (e == hipErrorNotReady) {
+        *ready = false;
+        return 0;
+    }
+    return fail_hip(c, "hipEventQuery(pinned ready)", e);
+}
+
+int pinned_mark_in_flight(Context* c, Pinned* p) {
+    if (!p->ready) return fail_msg(c, "pinned buffer has no ready event");
+    VMX_HIP(c, hipEventRecord(p->ready, c->stream));
+    p->in_flight = true;
+    return 0;
+}
+
 }  // namespace vmx
 
 using namespace vmx;
@@ -1155,7 +1190,13 @@ VMX_API int volta_cuda_pinned_alloc(void* raw, size_t bytes, uint64_t* out_id) {
         return 0;
     }
     void* ptr = nullptr;
-    VMX_HIP(c, hipHostMalloc(&ptr, bytes, hipHostMallocDefault));
+    hipEvent_t ready = nullptr;
+    VMX_HIP(c, hipEventCreateWithFlags(&ready, hipEventDisableTiming));
+    const hipError_t e = hipHostMalloc(&ptr, bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipEventDestroy(ready);
+        return fail_hip(c, "hipHostMalloc(pinned)", e);
+    }
     ++c->stats.pinned_allocation_calls;
     c->stats.live_pinned_bytes += bytes;
     c->stats.peak_pinned_bytes = std::max(c->stats.peak_pinned_bytes, c->stats.live_pinned_bytes);
@@ -1163,6 +1204,7 @@ VMX_API int volta_cuda_pinned_alloc(void* raw, size_t bytes, uint64_t* out_id) {
     const size_t slot = c->pinned.size() - 1;
     Pinned& p = c->pinned[slot];
     p.ptr = ptr;
+    p.ready = ready;
     p.capacity = bytes;
     p.logical = bytes;
     p.generation = 1;

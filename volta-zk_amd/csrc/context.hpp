@@ -260,6 +260,13 @@ int region_elems(Context* c, uint64_t id, size_t offset, size_t count, size_t el
 int strided_region(Context* c, uint64_t id, size_t offset, size_t stride, size_t row_bytes,
                    size_t rows, void** out, size_t* span);
 
+// Pinned host regions (byte offsets) and their transfer state: a pinned
+// source stays "in flight" from the copy that reads it until its ready event
+// completes (reference .cu:538-575).
+int pinned_region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out, Pinned** owner);
+int pinned_ready(Context* c, Pinned* p, bool* ready);
+int pinned_mark_in_flight(Context* c, Pinned* p);
+
 // ---- workspaces and twiddles ---------------------------------------------------
 int ensure_ws(Context* c, int slot, size_t bytes);
 template <typename T>

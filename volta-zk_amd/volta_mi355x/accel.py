@@ -137,6 +137,12 @@ _SIGS = {
     "volta_cuda_merkle_paths_device": (_int, [_vp, _u64, _sz, _sz, _u64, _sz, _sz, _u64, _sz]),
     "volta_cuda_hash_fp_columns": (_int, [_vp, _vp, _sz, _sz, _vp]),
     "volta_cuda_x4b_ntt_fp2": (_int, [_vp, _vp, _sz, _sz, _vp]),
+    "volta_cuda_pinned_alloc": (_int, [_vp, _sz, ctypes.POINTER(_u64)]),
+    "volta_cuda_pinned_write": (_int, [_vp, _u64, _sz, _vp, _sz]),
+    "volta_cuda_pinned_wait_ready": (_int, [_vp, _u64]),
+    "volta_cuda_pinned_free": (_int, [_vp, _u64]),
+    "volta_cuda_x4c_upload_pinned": (_int, [_vp, _u64, _sz, _u64, _sz, _sz]),
+    "volta_cuda_x4c_direct_fold_pinned_tile": (_int, [_vp, _u64, _sz, _u64, _sz, _sz, _sz, _sz, _sz, _u64, _u64]),
     "volta_cuda_x4c_direct_fold_arena": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _u64]),
     "volta_cuda_fp2_mobius_inverse_inplace_device": (_int, [_vp, _u64, _sz, _sz]),
     "volta_mi355x_x4_ntt_fp2_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz]),
@@ -673,6 +679,38 @@ class Backend:
             raise InvalidInput("X4c direct-fold input and output overlap")
         self._check(self.lib.volta_cuda_x4c_direct_fold_arena(self.raw, arena.id, input_offset_bytes, input_len,
                                                               output_offset_bytes, c0, c1))
+
+    # ---- pinned host pool and the X4c pinned transfers (lib.rs:4927-5027) -----------------
+    def pinned_alloc(self, nbytes: int) -> int:
+        out = ctypes.c_uint64()
+        self._check(self.lib.volta_cuda_pinned_alloc(self.raw, nbytes, ctypes.byref(out)))
+        return out.value
+
+    def pinned_write(self, pinned_id: int, offset_bytes: int, host: np.ndarray) -> None:
+        arr = np.ascontiguousarray(host)
+        self._check(self.lib.volta_cuda_pinned_write(self.raw, pinned_id, offset_bytes, arr.ctypes.data, arr.nbytes))
+
+    def pinned_wait_ready(self, pinned_id: int) -> None:
+        self._check(self.lib.volta_cuda_pinned_wait_ready(self.raw, pinned_id))
+
+    def pinned_free(self, pinned_id: int) -> None:
+        self._check(self.lib.volta_cuda_pinned_free(self.raw, pinned_id))
+
+    def x4c_upload_pinned(self, pinned_id: int, pinned_offset_bytes: int, arena: DeviceBuffer,
+                          arena_offset_bytes: int, nbytes: int) -> None:
+        self._own(arena)
+        self._check(self.lib.volta_cuda_x4c_upload_pinned(self.raw, pinned_id, pinned_offset_bytes, arena.id,
+                                                          arena_offset_bytes, nbytes))
+
+    def x4c_direct_fold_pinned_tile(self, pinned_id: int, pinned_offset_bytes: int, arena: DeviceBuffer,
+                                    output_offset_bytes: int, scratch_offset_bytes: int, input_len: int,
+                                    output_start: int, output_count: int, challenge) -> None:
+        """Outputs output_start.. of the fold of an input_len codeword from a pinned tile
+        holding output_count positive then output_count negative values (lib.rs:4927-4998)."""
+        self._own(arena)
+        self._check(self.lib.volta_cuda_x4c_direct_fold_pinned_tile(
+            self.raw, pinned_id, pinned_offset_bytes, arena.id, output_offset_bytes, scratch_offset_bytes, input_len,
+            output_start, output_count, int(challenge[0]), int(challenge[1])))
 
     def fp2_mobius_inverse_inplace_device(self, values: DeviceBuffer, offset: int = 0, n: int | None = None) -> None:
         """For every index bit, upper += lower (lib.rs:6601-6620)."""
