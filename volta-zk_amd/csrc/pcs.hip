@@ -56,11 +56,19 @@ int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows
 // - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
 // absorb up to 2^16 rows exactly; the fold to a field element happens once.
 
-constexpr int COMB_COLS = 8;       // columns per thread (one 16-byte i16 load)
-typedef uint32_t CombWords __attribute__((ext_vector_type(COMB_COLS / 2)));
 constexpr int COMB_THREADS = 256;
-constexpr size_t COMB_CHUNK = 128;  // rows per partial
-constexpr int COMB_UNROLL = 8;      // row loads kept in flight per thread
+constexpr size_t COMB_CHUNK = 128;  // rows per partial (u64 rows)
+
+// i16 rows: a workgroup's four waves share one tile of 64 x CI_COLS columns
+// and split the chunk's rows four ways; the waves' sums meet in LDS, so one
+// partial leaves per workgroup.  Four columns per thread keep the
+// accumulators at 64 VGPRs (4 waves per SIMD).
+constexpr int CI_COLS = 4;          // columns per thread (one 8-byte i16 load)
+typedef uint32_t CombWords __attribute__((ext_vector_type(CI_COLS / 2)));
+constexpr int CI_WAVES = 4;
+constexpr int CI_TILE = 64 * CI_COLS;  // columns per workgroup
+constexpr size_t CI_CHUNK = 512;    // rows per partial at most (128 per wave)
+constexpr int CI_UNROLL = 8;        // row loads kept in flight per thread
 
 // S[ck][comb][h] = sum over the chunk's rows of component h of coeff[comb][i]
 // (mod p): the 2^15 bias correction of the offset-binary trick below.
@@ -107,25 +115,29 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
                                                                    size_t rows, size_t cols, size_t msg_len,
                                                                    size_t comb0, size_t combinations, size_t chunk,
                                                                    int vec_ok) {
-    const size_t j0 = (static_cast<size_t>(blockIdx.x) * COMB_THREADS + threadIdx.x) * COMB_COLS;
+    __shared__ Fp2 red[CI_WAVES - 1][KC][CI_COLS][64];
+    // the wave index is uniform: row bounds and coefficient addresses stay scalar (SMEM loads)
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const size_t j0 = (static_cast<size_t>(blockIdx.x) * 64 + lane) * CI_COLS;
     const size_t ck = blockIdx.y;
-    const size_t r0 = ck * chunk;
-    const size_t r1 = min(rows, r0 + chunk);
-    uint64_t acc_lo[KC][2][COMB_COLS] = {};
-    uint64_t acc_hi[KC][2][COMB_COLS] = {};
-    const bool fast = (j0 + COMB_COLS <= cols) && vec_ok;
+    const size_t c0 = ck * chunk, c1 = min(rows, c0 + chunk);
+    const size_t per = (c1 - c0 + CI_WAVES - 1) / CI_WAVES;
+    const size_t r0 = min(c1, c0 + wave * per), r1 = min(c1, r0 + per);
+    uint64_t acc_lo[KC][2][CI_COLS] = {};
+    uint64_t acc_hi[KC][2][CI_COLS] = {};
+    const bool fast = (j0 + CI_COLS <= cols) && vec_ok;
     auto load = [&](size_t i, uint32_t* wp) {
         if (fast) {
-            // COMB_COLS i16 in one aligned vector load of COMB_COLS / 2 words
+            // CI_COLS i16 in one aligned vector load of CI_COLS / 2 words
             const CombWords raw = __builtin_nontemporal_load(reinterpret_cast<const CombWords*>(w + i * cols + j0));
 #pragma unroll
-            for (int q = 0; q < COMB_COLS / 2; ++q) {
+            for (int q = 0; q < CI_COLS / 2; ++q) {
                 wp[2 * q] = (raw[q] & 0xFFFFu) ^ 0x8000u;
                 wp[2 * q + 1] = (raw[q] >> 16) ^ 0x8000u;
             }
         } else {
 #pragma unroll
-            for (int q = 0; q < COMB_COLS; ++q) {
+            for (int q = 0; q < CI_COLS; ++q) {
                 const size_t j = j0 + q;
                 wp[q] = j < cols ? (static_cast<uint32_t>(static_cast<uint16_t>(w[i * cols + j])) ^ 0x8000u) : 0x8000u;
             }
@@ -141,7 +153,7 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
                 const uint32_t xl = static_cast<uint32_t>(comp[h]);
                 const uint32_t xh = static_cast<uint32_t>(comp[h] >> 32);
 #pragma unroll
-                for (int q = 0; q < COMB_COLS; ++q) {
+                for (int q = 0; q < CI_COLS; ++q) {
                     acc_lo[k][h][q] += static_cast<uint64_t>(xl) * wp[q];
                     acc_hi[k][h][q] += static_cast<uint64_t>(xh) * wp[q];
                 }
@@ -149,36 +161,46 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
         }
     };
     size_t i = r0;
-    for (; i + COMB_UNROLL <= r1; i += COMB_UNROLL) {
-        uint32_t wp[COMB_UNROLL][COMB_COLS];
+    for (; i + CI_UNROLL <= r1; i += CI_UNROLL) {
+        uint32_t wp[CI_UNROLL][CI_COLS];
 #pragma unroll
-        for (int u = 0; u < COMB_UNROLL; ++u) load(i + u, wp[u]);
+        for (int u = 0; u < CI_UNROLL; ++u) load(i + u, wp[u]);
 #pragma unroll
-        for (int u = 0; u < COMB_UNROLL; ++u) accumulate(i + u, wp[u]);
+        for (int u = 0; u < CI_UNROLL; ++u) accumulate(i + u, wp[u]);
     }
     for (; i < r1; ++i) {
-        uint32_t wp[COMB_COLS];
+        uint32_t wp[CI_COLS];
         load(i, wp);
         accumulate(i, wp);
     }
+    // this wave's sums as field elements: sum x w' = sum xl w' + 2^32 sum xh w'
     const uint64_t two32 = 0x100000000ull;
+    auto fold = [&](int k, int h, int q) {
+        return gl::add(gl::canon(acc_lo[k][h][q]), gl::mul(gl::canon(acc_hi[k][h][q]), two32));
+    };
+    if (wave > 0) {
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+#pragma unroll
+            for (int q = 0; q < CI_COLS; ++q) red[wave - 1][k][q][lane] = Fp2{fold(k, 0, q), fold(k, 1, q)};
+    }
+    __syncthreads();
+    if (wave > 0) return;
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
         if (comb0 + k >= combinations) break;
+        // the offset-binary bias of the whole chunk: 2^15 sum_i x_i
         uint64_t bias[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) bias[h] = gl::mul(sums[(ck * combinations + comb0 + k) * 2 + h], 0x8000ull);
 #pragma unroll
-        for (int q = 0; q < COMB_COLS; ++q) {
+        for (int q = 0; q < CI_COLS; ++q) {
             const size_t j = j0 + q;
             if (j >= cols) break;
-            uint64_t v[2];
+            Fp2 t{fold(k, 0, q), fold(k, 1, q)};
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint64_t t = gl::add(gl::canon(acc_lo[k][h][q]), gl::mul(gl::canon(acc_hi[k][h][q]), two32));
-                v[h] = gl::sub(t, bias[h]);
-            }
-            partials[(ck * combinations + comb0 + k) * msg_len + j] = Fp2{v[0], v[1]};
+            for (int o = 0; o < CI_WAVES - 1; ++o) t = gl::fp2_add(t, red[o][k][q][lane]);
+            partials[(ck * combinations + comb0 + k) * msg_len + j] = Fp2{gl::sub(t.c0, bias[0]), gl::sub(t.c1, bias[1])};
         }
     }
 }
@@ -286,11 +308,11 @@ static int launch_comb_groups(size_t combinations, F&& f) {
     return 0;
 }
 
-// Rows per partial: COMB_CHUNK, or fewer (down to 8) when the column blocks
-// times the chunks would not give about 1024 workgroups, so small matrices
-// still spread over the GPU's 256 CUs.  The reduce pass sums the chunks.
-static size_t comb_chunk(size_t rows, size_t col_blocks) {
-    size_t chunk = COMB_CHUNK;
+// Rows per partial: at most `largest`, or fewer (down to 8) when the column
+// blocks times the chunks would not give about 1024 workgroups, so small
+// matrices still spread over the GPU's 256 CUs.  The reduce pass sums the chunks.
+static size_t comb_chunk(size_t rows, size_t col_blocks, size_t largest = COMB_CHUNK) {
+    size_t chunk = largest;
     while (chunk > 8 && col_blocks * ((rows + chunk - 1) / chunk) < 1024) chunk >>= 1;
     return chunk;
 }
@@ -298,9 +320,8 @@ static size_t comb_chunk(size_t rows, size_t col_blocks) {
 int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
                      size_t cols, size_t pad, size_t combinations, Fp2* out) {
     const size_t msg_len = cols + pad;
-    const size_t col_threads = (cols + COMB_COLS - 1) / COMB_COLS;
-    const size_t col_blocks = (col_threads + COMB_THREADS - 1) / COMB_THREADS;
-    const size_t chunk = comb_chunk(rows, col_blocks);
+    const size_t col_blocks = (cols + CI_TILE - 1) / CI_TILE;
+    const size_t chunk = comb_chunk(rows, col_blocks, CI_CHUNK);
     const size_t chunks = (rows + chunk - 1) / chunk;
     size_t per_chunk = 0, bytes = 0, sum_bytes = 0;
     if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes) ||
@@ -316,8 +337,8 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
                        dim3(256), 0, c->stream, coeffs, sums, rows, chunk);
     VMX_HIP(c, hipGetLastError());
     const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
-    // Vector row loads need a base and a row pitch aligned to COMB_COLS i16.
-    const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * COMB_COLS) == 0) && (cols % COMB_COLS == 0);
+    // Vector row loads need a base and a row pitch aligned to CI_COLS i16.
+    const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * CI_COLS) == 0) && (cols % CI_COLS == 0);
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
             if (kc == 2)
                 hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
