@@ -140,10 +140,12 @@ def test_linearity_ties_combination_to_encode(backend, oracle):
 
 # ---- small primitives ----------------------------------------------------------------
 
-@pytest.mark.parametrize("count", [1, 7, 255, 2049, 70001])
+@pytest.mark.parametrize("count", [1, 7, 64, 255, 4097, 70001, (1 << 18) - 1, 1 << 18, 300001])
 def test_fp2_powers_counts(backend, oracle, count):
-    """c^(i+1) as the product of c^(2^k) over the set bits of i+1: a single
-    element, partial blocks and several grid strides match the serial powers."""
+    """c^(i+1) from the three-level table (below 2^18 powers, its last entry
+    included) or from the squarings over the set bits of i+1 (2^18 and up):
+    a single element, partial blocks and several grid strides match the
+    serial powers."""
     c = (123456789123, int(P - 5))
     d = backend.fp2_powers_device(c, count)
     got = backend.download_device(d).view(np.uint64).reshape(-1, 2)

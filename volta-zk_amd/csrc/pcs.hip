@@ -422,7 +422,37 @@ __global__ void fp2_powers_kernel(Fp2Squares sq, Fp2* out, size_t count, int bit
     }
 }
 
+// Below 2^18 powers: c^e = T0[e mod 64] T1[(e >> 6) mod 64] T2[e >> 12] with
+// T_l[j] = c^(j 64^l), built on the host and passed by value (3 KiB of the
+// 4 KiB argument space); two products per element, no divergence.
+constexpr int POW_LEVELS = 3;
+constexpr size_t POW_TABLE_LIMIT = size_t{1} << (6 * POW_LEVELS);
+struct Fp2PowTable {
+    Fp2 t[POW_LEVELS][64];
+};
+
+__global__ void fp2_powers_table_kernel(Fp2PowTable tb, Fp2* out, size_t count) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const size_t e = i + 1;  // < 2^18
+        out[i] = gl::fp2_mul(gl::fp2_mul(tb.t[0][e & 63], tb.t[1][(e >> 6) & 63]), tb.t[2][e >> 12]);
+    }
+}
+
 int fp2_powers(Context* c, Fp2 base, Fp2* out, size_t count) {
+    if (count < POW_TABLE_LIMIT) {
+        Fp2PowTable tb;
+        Fp2 step = base;  // c^(64^l)
+        for (int l = 0; l < POW_LEVELS; ++l) {
+            tb.t[l][0] = Fp2{1, 0};
+            for (int j = 1; j < 64; ++j) tb.t[l][j] = gl::fp2_mul(tb.t[l][j - 1], step);
+            step = gl::fp2_mul(tb.t[l][63], step);
+        }
+        hipLaunchKernelGGL(fp2_powers_table_kernel, dim3(grid_for(count, 256, 8192)), dim3(256), 0, c->stream, tb,
+                           out, count);
+        VMX_HIP(c, hipGetLastError());
+        return 0;
+    }
     Fp2Squares sq{};
     int bits = 0;
     while (bits < 64 && (count >> bits) != 0) ++bits;  // bit length of count >= bit length of i + 1
