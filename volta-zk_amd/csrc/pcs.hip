@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "chacha8.hpp"
 #include "context.hpp"
@@ -125,24 +126,6 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
     const size_t r0 = min(c1, c0 + wave * per), r1 = min(c1, r0 + per);
     uint64_t acc_lo[KC][2][CI_COLS] = {};
     uint64_t acc_hi[KC][2][CI_COLS] = {};
-    const bool fast = (j0 + CI_COLS <= cols) && vec_ok;
-    auto load = [&](size_t i, uint32_t* wp) {
-        if (fast) {
-            // CI_COLS i16 in one aligned vector load of CI_COLS / 2 words
-            const CombWords raw = __builtin_nontemporal_load(reinterpret_cast<const CombWords*>(w + i * cols + j0));
-#pragma unroll
-            for (int q = 0; q < CI_COLS / 2; ++q) {
-                wp[2 * q] = (raw[q] & 0xFFFFu) ^ 0x8000u;
-                wp[2 * q + 1] = (raw[q] >> 16) ^ 0x8000u;
-            }
-        } else {
-#pragma unroll
-            for (int q = 0; q < CI_COLS; ++q) {
-                const size_t j = j0 + q;
-                wp[q] = j < cols ? (static_cast<uint32_t>(static_cast<uint16_t>(w[i * cols + j])) ^ 0x8000u) : 0x8000u;
-            }
-        }
-    };
     auto accumulate = [&](size_t i, const uint32_t* wp) {
 #pragma unroll
         for (int k = 0; k < KC; ++k) {
@@ -160,19 +143,46 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
             }
         }
     };
-    size_t i = r0;
-    for (; i + CI_UNROLL <= r1; i += CI_UNROLL) {
-        uint32_t wp[CI_UNROLL][CI_COLS];
+    // The vector/scalar load choice is made once, outside the row loop, so the
+    // loop body has no branches and its CI_UNROLL row loads are all in flight
+    // together.
+    auto rows_loop = [&](auto fast_tag) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        auto load = [&](size_t i, uint32_t* wp) {
+            if constexpr (FAST) {
+                // CI_COLS i16 in one aligned vector load of CI_COLS / 2 words
+                const CombWords raw =
+                    __builtin_nontemporal_load(reinterpret_cast<const CombWords*>(w + i * cols + j0));
 #pragma unroll
-        for (int u = 0; u < CI_UNROLL; ++u) load(i + u, wp[u]);
+                for (int q = 0; q < CI_COLS / 2; ++q) {
+                    wp[2 * q] = (raw[q] & 0xFFFFu) ^ 0x8000u;
+                    wp[2 * q + 1] = (raw[q] >> 16) ^ 0x8000u;
+                }
+            } else {
 #pragma unroll
-        for (int u = 0; u < CI_UNROLL; ++u) accumulate(i + u, wp[u]);
-    }
-    for (; i < r1; ++i) {
-        uint32_t wp[CI_COLS];
-        load(i, wp);
-        accumulate(i, wp);
-    }
+                for (int q = 0; q < CI_COLS; ++q) {
+                    const size_t j = min(j0 + q, cols - 1);  // in bounds; masked below
+                    const uint32_t x = static_cast<uint32_t>(static_cast<uint16_t>(w[i * cols + j])) ^ 0x8000u;
+                    wp[q] = j0 + q < cols ? x : 0x8000u;
+                }
+            }
+        };
+        size_t i = r0;
+        for (; i + CI_UNROLL <= r1; i += CI_UNROLL) {
+            uint32_t wp[CI_UNROLL][CI_COLS];
+#pragma unroll
+            for (int u = 0; u < CI_UNROLL; ++u) load(i + u, wp[u]);
+#pragma unroll
+            for (int u = 0; u < CI_UNROLL; ++u) accumulate(i + u, wp[u]);
+        }
+        for (; i < r1; ++i) {
+            uint32_t wp[CI_COLS];
+            load(i, wp);
+            accumulate(i, wp);
+        }
+    };
+    if ((j0 + CI_COLS <= cols) && vec_ok) rows_loop(std::true_type{});
+    else rows_loop(std::false_type{});
     // this wave's sums as field elements: sum x w' = sum xl w' + 2^32 sum xh w'
     const uint64_t two32 = 0x100000000ull;
     auto fold = [&](int k, int h, int q) {
