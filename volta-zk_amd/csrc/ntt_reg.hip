@@ -54,8 +54,11 @@ constexpr int ew_log() {
 }
 
 // w_4096^e for e < 4096 from the inner table (w_4096^j, j < 2048; w_4096^2048 = -1).
+// The load is unconditional and the sign a select, so no branch splits a
+// tile's loads.
 __device__ __forceinline__ uint64_t inner_pow(const uint64_t* inner, uint32_t e) {
-    return e < 2048 ? inner[e] : gl::neg(inner[e - 2048]);
+    const uint64_t v = inner[e & 2047];
+    return (e & 2048) ? gl::neg(v) : v;
 }
 
 // The partner lane's value (lane ^ 1): the other coordinate of the same element.
@@ -91,18 +94,30 @@ __device__ __forceinline__ void unpark(const uint64_t* s, uint64_t* v, uint32_t 
 }
 
 // Inputs of the gather pass.  Row `row` of a batch, element idx < n,
-// coordinate `plane`:
+// coordinate `plane`.  fetch() only loads (from an index clamped into the
+// row, so every load is unconditional and in bounds); finish() masks the
+// zero tail and applies any scaling, after all of a tile's loads are issued.
 // SrcU64: x + row x_stride elements of PL u64, len elements then zeros; with
 //   reverse the transform reads index (n - idx) mod n (the inverse transform
 //   as a forward one) and every input is multiplied by scale unless it is 1.
+//   len >= 1 (the host substitutes a one-word zero source for len = 0).
 struct SrcU64 {
     const uint64_t* x;
     uint64_t x_stride, len;
     int reverse;
     uint64_t scale;
-    __device__ __forceinline__ uint64_t load(uint64_t row, uint64_t idx, uint32_t plane, int PL, uint64_t nmask) const {
-        if (reverse) idx = (uint64_t{0} - idx) & nmask;
-        uint64_t v = idx < len ? x[(row * x_stride + idx) * PL + plane] : 0;
+    struct Raw {
+        uint64_t v;
+    };
+    __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t nmask) const {
+        return reverse ? (uint64_t{0} - idx) & nmask : idx;
+    }
+    __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t plane, int PL) const {
+        const uint64_t ci = idx < len ? idx : 0;
+        return Raw{x[(row * x_stride + ci) * PL + plane]};
+    }
+    __device__ __forceinline__ uint64_t finish(uint64_t idx, Raw r) const {
+        uint64_t v = idx < len ? r.v : 0;
         if (scale != 1) v = gl::mul32x4(v, scale);
         return v;
     }
@@ -110,14 +125,24 @@ struct SrcU64 {
 // SrcMsgI16: the Ligero message row lift(w) || pads || 0 (reference
 //   pcs_messages_kernel, cuda/volta_cuda_backend.cu:2950-2958): cols i16
 //   weights lifted as signed residues, then pad u64 pads, then zeros.
+//   w and pads always point at readable words: for cols = 0 or pad = 0 the
+//   host points them at the inner table, whose words are then masked out.
 struct SrcMsgI16 {
     const int16_t* w;
     const uint64_t* pads;
     uint64_t cols, pad;
-    __device__ __forceinline__ uint64_t load(uint64_t row, uint64_t idx, uint32_t, int, uint64_t) const {
-        if (idx < cols) return gl::from_i16(w[row * cols + idx]);
-        if (idx < cols + pad) return pads[row * pad + (idx - cols)];
-        return 0;
+    struct Raw {
+        int16_t w;
+        uint64_t p;
+    };
+    __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t) const { return idx; }
+    __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t, int) const {
+        const uint64_t wi = idx < cols ? idx : 0;
+        const uint64_t pi = idx >= cols && idx - cols < pad ? idx - cols : 0;
+        return Raw{w[row * cols + wi], pads[row * pad + pi]};
+    }
+    __device__ __forceinline__ uint64_t finish(uint64_t idx, Raw r) const {
+        return idx < cols ? gl::from_i16(r.w) : idx - cols < pad ? r.p : 0;
     }
 };
 
@@ -141,11 +166,17 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
+        typename Src::Raw raw[A];
+        gl::static_for<0, A>([&](auto ja_) {
+            constexpr int ja = decltype(ja_)::value;
+            const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
+            raw[ja] = src.fetch(row, idx, plane, PL);
+        });
         uint64_t v[A];
         gl::static_for<0, A>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
-            const uint64_t idx = nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh);
-            v[gl::bitrev_c(ja, LA)] = src.load(row, idx, plane, PL, nmask);
+            const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
+            v[gl::bitrev_c(ja, LA)] = src.finish(idx, raw[ja]);
         });
         gl::dit_pow2<LA, ew_log<LA>()>(v);
         park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
@@ -171,9 +202,10 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
 // gets the R-point DFT over i.  For an X4 transform of 2^33 points the last
 // pass (hb = 0) meets imaginary twiddles, which mix the two coordinates: each
 // lane then also reads its partner lane's coordinate.
-template <int LA, int LB, int PL>
+template <int LA, int LB, int PL, int MODE>
 __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, int lb, int cb, const uint64_t* inner,
                                                    const uint64_t* split, int split_h) {
+    static_assert(PL == 2 || MODE == ROOT_BASE, "one-plane transforms stop at 2^31 points");
     constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
     extern __shared__ uint64_t s[];
     a += (static_cast<uint64_t>(blockIdx.y) << nb) * PL;
@@ -185,7 +217,7 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
     const uint64_t h = blk / lblocks;
     const uint64_t l0 = (blk - h * lblocks) << cb;
     const uint64_t base = ((h << RB) << lb) + l0;
-    const bool mixed = PL == 2 && nb == 33 && hb == 0;  // uniform
+    const bool mixed = MODE == ROOT_IMAG33 && hb == 0;  // uniform
     for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
@@ -196,9 +228,9 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
             const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
             const uint64_t xv = a[PL * (base + (i << lb) + c) + plane];
             bool imag;
-            const uint64_t t = root_pow((i * l) << hb, nb, split, split_h, imag);
+            const uint64_t t = root_pow<MODE>((i * l) << hb, split, split_h, imag);
             uint64_t r;
-            if constexpr (PL == 2) {
+            if constexpr (MODE == ROOT_IMAG33) {
                 if (mixed) {
                     const uint64_t other = partner(xv);
                     // (v0 + v1 phi) (t phi) = 7 v1 t + v0 t phi
@@ -252,22 +284,32 @@ template <class Src>
 using GatherFn = void (*)(Src, uint64_t*, int, int, nreg::Digits, const uint64_t*);
 using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int);
 
+template <int LA, int LB, int PL>
+ColFn col_for(int mode) {
+    if constexpr (PL == 2) {
+        if (mode == nreg::ROOT_NEG32) return nreg::col_reg<LA, LB, PL, nreg::ROOT_NEG32>;
+        if (mode == nreg::ROOT_IMAG33) return nreg::col_reg<LA, LB, PL, nreg::ROOT_IMAG33>;
+    }
+    return mode == nreg::ROOT_BASE ? nreg::col_reg<LA, LB, PL, nreg::ROOT_BASE> : nullptr;
+}
+
 template <int PL, class Src>
-bool kernels_for(int rb, GatherFn<Src>* g, ColFn* col) {
+bool kernels_for(int rb, int mode, GatherFn<Src>* g, ColFn* col) {
     switch (rb) {
-        case 5: *g = nreg::gather_reg<3, 2, PL, Src>; *col = nreg::col_reg<3, 2, PL>; return true;
-        case 6: *g = nreg::gather_reg<3, 3, PL, Src>; *col = nreg::col_reg<3, 3, PL>; return true;
-        case 7: *g = nreg::gather_reg<4, 3, PL, Src>; *col = nreg::col_reg<4, 3, PL>; return true;
-        case 8: *g = nreg::gather_reg<4, 4, PL, Src>; *col = nreg::col_reg<4, 4, PL>; return true;
+        case 5: *g = nreg::gather_reg<3, 2, PL, Src>; *col = col_for<3, 2, PL>(mode); break;
+        case 6: *g = nreg::gather_reg<3, 3, PL, Src>; *col = col_for<3, 3, PL>(mode); break;
+        case 7: *g = nreg::gather_reg<4, 3, PL, Src>; *col = col_for<4, 3, PL>(mode); break;
+        case 8: *g = nreg::gather_reg<4, 4, PL, Src>; *col = col_for<4, 4, PL>(mode); break;
         case 9:
             if constexpr (PL == 1) {
                 *g = nreg::gather_reg<5, 4, PL, Src>;
-                *col = nreg::col_reg<5, 4, PL>;
-                return true;
+                *col = col_for<5, 4, PL>(mode);
+                break;
             }
             return false;
         default: return false;
     }
+    return *col != nullptr;
 }
 
 // Pass radices: the fewest passes of at most 2^pass_bits, as even as possible.
@@ -346,7 +388,7 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             for (int j = 0; j < d.count; ++j) d.bits[j] = r[1 + j];
             const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
             const size_t lds = tile_lds(rb, qb + PL - 1);
-            if (!kernels_for<PL, Src>(rb, &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, g, lds)) return -1;
             hipLaunchKernelGGL(g, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, s0, y,
@@ -359,7 +401,7 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             const int cb = std::min(wb, lb);
             const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
             const size_t lds = tile_lds(rb, cb + PL - 1);
-            if (!kernels_for<PL, Src>(rb, &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, col, lds)) return -1;
             hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
@@ -374,7 +416,8 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
 int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_stride, uint64_t len, uint64_t* out,
             uint64_t rows, int nb, int planes, bool inverse) {
     if (inverse && nb > 31) return fail_msg(c, "inverse transforms are defined up to 2^31 points");
-    const nreg::SrcU64 src{in, in_stride, len, inverse ? 1 : 0,
+    // a zero-length input reads one in-bounds word of the inner table, masked to zero
+    const nreg::SrcU64 src{len ? in : tb.inner, len ? in_stride : 0, len ? len : 1, inverse ? 1 : 0,
                            inverse ? gl::inv_host(gl::canon(uint64_t{1} << nb)) : uint64_t{1}};
     auto shift1 = [](nreg::SrcU64 s, uint64_t r0) {  // to the launch slice's first row
         s.x += r0 * s.x_stride;
@@ -391,7 +434,8 @@ int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_str
 
 int reg_ntt_msg_i16(Context* c, const RegTables& tb, const int16_t* w, const uint64_t* pads, uint64_t cols,
                     uint64_t pad, uint64_t* out, uint64_t rows, int nb) {
-    const nreg::SrcMsgI16 src{w, pads, cols, pad};
+    const nreg::SrcMsgI16 src{cols ? w : reinterpret_cast<const int16_t*>(tb.inner), pad ? pads : tb.inner, cols,
+                              pad};
     auto shift = [](nreg::SrcMsgI16 s, uint64_t r0) {
         s.w += r0 * s.cols;
         if (s.pad) s.pads += r0 * s.pad;

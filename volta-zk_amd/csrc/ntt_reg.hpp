@@ -62,24 +62,39 @@ __device__ __forceinline__ uint64_t tw_split(const uint64_t* t, uint64_t e, int 
 // 7 x = 8 x - x.
 __device__ __forceinline__ uint64_t mul7(uint64_t x) { return gl::sub(gl::shl_mod<3>(x), x); }
 
-// w(2^nb)^e for e < 2^nb, nb <= 33, from the two-level table of
-// b_min(nb,32): the real value, or (imag set) the c1 coordinate of a purely
-// imaginary power (nb = 33, e odd).
-__device__ __forceinline__ uint64_t root_pow(uint64_t e, int nb, const uint64_t* split, int h, bool& imag) {
+// Which X4 root a transform of 2^nb points uses: the base root (nb <= 31),
+// the negated one (nb = 32) or the imaginary one (nb = 33).  A kernel is
+// compiled per mode so the per-element twiddle code has no branches and its
+// table loads can all be in flight together.
+enum RootMode { ROOT_BASE = 0, ROOT_NEG32 = 1, ROOT_IMAG33 = 2 };
+constexpr int root_mode(int nb) { return nb <= 31 ? ROOT_BASE : nb == 32 ? ROOT_NEG32 : ROOT_IMAG33; }
+
+// w(2^nb)^e for e < 2^nb from the two-level table of b_min(nb,32): the real
+// value, or (imag set) the c1 coordinate of a purely imaginary power (nb = 33,
+// e odd).
+template <int MODE>
+__device__ __forceinline__ uint64_t root_pow(uint64_t e, const uint64_t* split, int h, bool& imag) {
     imag = false;
-    if (nb <= 31) return tw_split(split, e, h);
-    if (nb == 32) {
+    if constexpr (MODE == ROOT_BASE) {
+        return tw_split(split, e, h);
+    } else if constexpr (MODE == ROOT_NEG32) {
         const uint64_t v = tw_split(split, e, h);
         return (e & 1) ? gl::neg(v) : v;
+    } else {
+        const uint64_t q = e >> 1;
+        uint64_t t = tw_split(split, q, h);
+        if (q & 1) t = gl::neg(t);
+        imag = (e & 1) != 0;
+        const uint64_t ti = gl::mul32x4(ROOT33_C1, t);
+        return imag ? ti : t;
     }
-    const uint64_t q = e >> 1;
-    uint64_t t = tw_split(split, q, h);
-    if (q & 1) t = gl::neg(t);
-    if (e & 1) {
-        imag = true;
-        return gl::mul32x4(ROOT33_C1, t);
-    }
-    return t;
+}
+
+// The same for a transform size known only at run time (the fold kernel).
+__device__ __forceinline__ uint64_t root_pow(uint64_t e, int nb, const uint64_t* split, int h, bool& imag) {
+    if (nb <= 31) return root_pow<ROOT_BASE>(e, split, h, imag);
+    if (nb == 32) return root_pow<ROOT_NEG32>(e, split, h, imag);
+    return root_pow<ROOT_IMAG33>(e, split, h, imag);
 }
 
 // Mixed-radix layout of a row index of the gather pass.
