@@ -222,25 +222,47 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
         const uint64_t l = l0 + c;
+        // all of this job's loads first (data and both twiddle-table words),
+        // then the arithmetic: the loads are in flight together
+        uint64_t xv[A], tlo[A], thi[A];
+        const uint64_t hmask = (uint64_t{1} << split_h) - 1;
+        gl::static_for<0, A>([&](auto ja_) {
+            constexpr int ja = decltype(ja_)::value;
+            const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+            xv[ja] = a[PL * (base + (i << lb) + c) + plane];
+            const uint64_t e = (i * l) << hb;
+            const uint64_t q = MODE == ROOT_IMAG33 ? e >> 1 : e;
+            tlo[ja] = split[q & hmask];
+            thi[ja] = split[hmask + 1 + (q >> split_h)];
+        });
+        __builtin_amdgcn_sched_barrier(0);
         uint64_t v[A];
         gl::static_for<0, A>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
             const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
-            const uint64_t xv = a[PL * (base + (i << lb) + c) + plane];
-            bool imag;
-            const uint64_t t = root_pow<MODE>((i * l) << hb, split, split_h, imag);
+            const uint64_t e = (i * l) << hb;
+            uint64_t t = gl::mul32x4(tlo[ja], thi[ja]);
+            bool imag = false;
+            if constexpr (MODE == ROOT_NEG32) {
+                t = (e & 1) ? gl::neg(t) : t;
+            } else if constexpr (MODE == ROOT_IMAG33) {
+                if ((e >> 1) & 1) t = gl::neg(t);
+                imag = (e & 1) != 0;
+                const uint64_t ti = gl::mul32x4(ROOT33_C1, t);
+                t = imag ? ti : t;
+            }
+            const uint64_t xvv = xv[ja];
             uint64_t r;
             if constexpr (MODE == ROOT_IMAG33) {
                 if (mixed) {
-                    const uint64_t other = partner(xv);
-                    // (v0 + v1 phi) (t phi) = 7 v1 t + v0 t phi
-                    r = !imag ? gl::mul32x4(xv, t)
+                    const uint64_t other = partner(xvv);
+                    r = !imag ? gl::mul32x4(xvv, t)
                               : plane == 0 ? mul7(gl::mul32x4(other, t)) : gl::mul32x4(other, t);
                 } else {
-                    r = gl::mul32x4(xv, t);
+                    r = gl::mul32x4(xvv, t);
                 }
             } else {
-                r = gl::mul32x4(xv, t);
+                r = gl::mul32x4(xvv, t);
             }
             v[gl::bitrev_c(ja, LA)] = r;
         });
