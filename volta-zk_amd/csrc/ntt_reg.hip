@@ -222,50 +222,78 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
         const uint64_t l = l0 + c;
-        // all of this job's loads first (data and both twiddle-table words),
-        // then the arithmetic: the loads are in flight together
-        uint64_t xv[A], tlo[A], thi[A];
-        const uint64_t hmask = (uint64_t{1} << split_h) - 1;
-        gl::static_for<0, A>([&](auto ja_) {
-            constexpr int ja = decltype(ja_)::value;
-            const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
-            xv[ja] = a[PL * (base + (i << lb) + c) + plane];
-            const uint64_t e = (i * l) << hb;
-            const uint64_t q = MODE == ROOT_IMAG33 ? e >> 1 : e;
-            tlo[ja] = split[q & hmask];
-            thi[ja] = split[hmask + 1 + (q >> split_h)];
-        });
-        __builtin_amdgcn_sched_barrier(0);
         uint64_t v[A];
-        gl::static_for<0, A>([&](auto ja_) {
-            constexpr int ja = decltype(ja_)::value;
-            const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
-            const uint64_t e = (i * l) << hb;
-            uint64_t t = gl::mul32x4(tlo[ja], thi[ja]);
-            bool imag = false;
-            if constexpr (MODE == ROOT_NEG32) {
-                t = (e & 1) ? gl::neg(t) : t;
-            } else if constexpr (MODE == ROOT_IMAG33) {
-                if ((e >> 1) & 1) t = gl::neg(t);
-                imag = (e & 1) != 0;
-                const uint64_t ti = gl::mul32x4(ROOT33_C1, t);
-                t = imag ? ti : t;
+        if constexpr (MODE != ROOT_IMAG33) {
+            // real roots: the pre-twiddles w^(H l (ja B + jb)) are t0 s^ja with
+            // t0 = w^(H l jb) and s = w^(H l B); the job loads its A inputs and
+            // four table words, then multiplies along the progression
+            uint64_t xv[A];
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+                xv[ja] = a[PL * (base + (i << lb) + c) + plane];
+            });
+            const uint64_t e0 = (static_cast<uint64_t>(jb) * l) << hb, es = (static_cast<uint64_t>(B) * l) << hb;
+            const uint64_t hmask = (uint64_t{1} << split_h) - 1;
+            const uint64_t p0 = split[e0 & hmask], q0 = split[hmask + 1 + (e0 >> split_h)];
+            const uint64_t p1 = split[es & hmask], q1 = split[hmask + 1 + (es >> split_h)];
+            __builtin_amdgcn_sched_barrier(0);  // every load of the job is in flight before the arithmetic
+            uint64_t t = gl::mul32x4(p0, q0);
+            uint64_t st = gl::mul32x4(p1, q1);
+            if constexpr (MODE == ROOT_NEG32) {  // w(2^32)^e = (-1)^e b_32^e
+                if (e0 & 1) t = gl::neg(t);
+                if (es & 1) st = gl::neg(st);
             }
-            const uint64_t xvv = xv[ja];
-            uint64_t r;
-            if constexpr (MODE == ROOT_IMAG33) {
-                if (mixed) {
-                    const uint64_t other = partner(xvv);
-                    r = !imag ? gl::mul32x4(xvv, t)
-                              : plane == 0 ? mul7(gl::mul32x4(other, t)) : gl::mul32x4(other, t);
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                v[gl::bitrev_c(ja, LA)] = gl::mul32x4(xv[ja], t);
+                if constexpr (ja + 1 < A) t = gl::mul32x4(t, st);
+            });
+        } else {
+            // all of this job's loads first (data and both twiddle-table words),
+            // then the arithmetic: the loads are in flight together
+            uint64_t xv[A], tlo[A], thi[A];
+            const uint64_t hmask = (uint64_t{1} << split_h) - 1;
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+                xv[ja] = a[PL * (base + (i << lb) + c) + plane];
+                const uint64_t e = (i * l) << hb;
+                const uint64_t q = MODE == ROOT_IMAG33 ? e >> 1 : e;
+                tlo[ja] = split[q & hmask];
+                thi[ja] = split[hmask + 1 + (q >> split_h)];
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+                const uint64_t e = (i * l) << hb;
+                uint64_t t = gl::mul32x4(tlo[ja], thi[ja]);
+                bool imag = false;
+                if constexpr (MODE == ROOT_NEG32) {
+                    t = (e & 1) ? gl::neg(t) : t;
+                } else if constexpr (MODE == ROOT_IMAG33) {
+                    if ((e >> 1) & 1) t = gl::neg(t);
+                    imag = (e & 1) != 0;
+                    const uint64_t ti = gl::mul32x4(ROOT33_C1, t);
+                    t = imag ? ti : t;
+                }
+                const uint64_t xvv = xv[ja];
+                uint64_t r;
+                if constexpr (MODE == ROOT_IMAG33) {
+                    if (mixed) {
+                        const uint64_t other = partner(xvv);
+                        r = !imag ? gl::mul32x4(xvv, t)
+                                  : plane == 0 ? mul7(gl::mul32x4(other, t)) : gl::mul32x4(other, t);
+                    } else {
+                        r = gl::mul32x4(xvv, t);
+                    }
                 } else {
                     r = gl::mul32x4(xvv, t);
                 }
-            } else {
-                r = gl::mul32x4(xvv, t);
-            }
-            v[gl::bitrev_c(ja, LA)] = r;
-        });
+                v[gl::bitrev_c(ja, LA)] = r;
+            });
+        }
         gl::dit_pow2<LA, ew_log<LA>()>(v);
         park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
     }
