@@ -179,6 +179,21 @@ def test_compact_encode_device(backend, oracle):
         assert (got == oracle.ntt_encode_batch(msgs, n)).all()
 
 
+@pytest.mark.parametrize("n", [1 << 12, 1 << 14, 1 << 16])
+def test_encode_of_empty_messages_is_zero(backend, n):
+    """msg_len = 0, which the seam accepts: every codeword is zero on the
+    one-tile path (2^12) and on the pass engine, whose loads still read an
+    in-bounds word and mask it."""
+    d = backend.upload_device(np.array([12345], dtype=np.uint64))
+    out = backend.ntt_fp_encode_device(d, 3, 0, n)
+    got = backend.download_device(out)
+    backend.free_device(d)
+    backend.free_device(out)
+    assert got.shape == (3 * n,) and not got.any()
+    host = backend.ntt_fp_batch(np.zeros(0, np.uint64), 2, 0, n)
+    assert not np.asarray(host).any()
+
+
 # ---- PCS encode of i16 message rows ---------------------------------------------------
 
 @pytest.mark.parametrize("rows,cols,pad,bits", [(5, 16, 0, 6), (9, 100, 7, 8), (17, 2048, 0, 13), (4, 2048, 512, 13),

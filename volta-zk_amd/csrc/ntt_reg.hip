@@ -100,7 +100,8 @@ __device__ __forceinline__ void unpark(const uint64_t* s, uint64_t* v, uint32_t 
 // SrcU64: x + row x_stride elements of PL u64, len elements then zeros; with
 //   reverse the transform reads index (n - idx) mod n (the inverse transform
 //   as a forward one) and every input is multiplied by scale unless it is 1.
-//   len >= 1 (the host substitutes a one-word zero source for len = 0).
+//   For len = 0 the host points x at the inner table with stride 0: fetch()
+//   reads its word 0, and finish() masks every input to zero.
 struct SrcU64 {
     const uint64_t* x;
     uint64_t x_stride, len;
@@ -467,7 +468,7 @@ int reg_ntt(Context* c, const RegTables& tb, const uint64_t* in, uint64_t in_str
             uint64_t rows, int nb, int planes, bool inverse) {
     if (inverse && nb > 31) return fail_msg(c, "inverse transforms are defined up to 2^31 points");
     // a zero-length input reads one in-bounds word of the inner table, masked to zero
-    const nreg::SrcU64 src{len ? in : tb.inner, len ? in_stride : 0, len ? len : 1, inverse ? 1 : 0,
+    const nreg::SrcU64 src{len ? in : tb.inner, len ? in_stride : 0, len, inverse ? 1 : 0,
                            inverse ? gl::inv_host(gl::canon(uint64_t{1} << nb)) : uint64_t{1}};
     auto shift1 = [](nreg::SrcU64 s, uint64_t r0) {  // to the launch slice's first row
         s.x += r0 * s.x_stride;
