@@ -21,17 +21,13 @@ constexpr uint64_t EPS = 0x00000000FFFFFFFFull;
 
 __host__ __device__ __forceinline__ uint64_t canon(uint64_t x) { return x >= P ? x - P : x; }
 
-// s = a + b; the result is s - p exactly when a + b >= p, i.e. when the sum
-// carries out of 64 bits or s + eps does (s >= 2^64 - eps = p); s - p is then
-// s + eps mod 2^64.  Written on 32-bit carry chains (v_add_co/v_addc).
+// t = a + b and s = t + eps (mod 2^64).  s wraps past 2^64 exactly when
+// a + b >= p (b + eps < 2^64 for b < p), and then s = a + b - p < a; otherwise
+// s >= a and the sum is t.  Two 64-bit adds, one compare, one select.
 __host__ __device__ __forceinline__ uint64_t add(uint64_t a, uint64_t b) {
-    unsigned c0, c1, d0, d1;
-    const uint32_t s0 = __builtin_addc(static_cast<uint32_t>(a), static_cast<uint32_t>(b), 0u, &c0);
-    const uint32_t s1 = __builtin_addc(static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32), c0, &c1);
-    const uint32_t t0 = __builtin_addc(s0, 0xFFFFFFFFu, 0u, &d0);
-    const uint32_t t1 = __builtin_addc(s1, 0u, d0, &d1);
-    const bool over = (c1 | d1) != 0;
-    return (static_cast<uint64_t>(over ? t1 : s1) << 32) | (over ? t0 : s0);
+    const uint64_t t = a + b;
+    const uint64_t s = t + EPS;
+    return s < a ? s : t;
 }
 
 // d = a - b; a borrow out of 64 bits is worth -2^64 = -eps, i.e. d - eps,
