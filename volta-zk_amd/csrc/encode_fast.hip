@@ -44,21 +44,23 @@ constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 // past cols.  A raw buffer resource spanning exactly the row's cols entries
 // makes the hardware return 0 for the tail (an out-of-range buffer load reads
 // zero and touches no memory), and all 32 loads share one offset register.
-__device__ __forceinline__ void load_column(const int16_t* wr, size_t cols, int i2, int32_t* x) {
+__device__ __forceinline__ void load_column(const int16_t* wr, size_t cols, int i2, uint32_t* x) {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<int16_t*>(wr), static_cast<short>(0), static_cast<int>(cols * sizeof(int16_t)), 0x00020000);
     const int off = i2 * static_cast<int>(sizeof(int16_t));
 #pragma unroll
-    for (int i1 = 0; i1 < K; ++i1)
-        x[i1] = static_cast<int16_t>(  // the builtin returns the 16 bits unsigned
-            __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + i1 * N2 * static_cast<int>(sizeof(int16_t)), 0, 0));
+    for (int q = 0; q < K / 2; ++q) {  // x[q] = w[2q] | w[2q + 1] << 16 (two i16 per register)
+        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + 2 * q * N2 * static_cast<int>(sizeof(int16_t)), 0, 0);
+        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + (2 * q + 1) * N2 * static_cast<int>(sizeof(int16_t)), 0, 0);
+        x[q] = (lo & 0xFFFFu) | (hi << 16);
+    }
 }
 
 // Phase A for coset S and column i2 of one row: writes Y[4 t1 + S][i2].
 // The four-step twiddles w_n^(i2 (4 t1 + S)) come from the L2-resident grid;
 // their loads are issued before the DFT so its arithmetic covers the latency.
 template <int S>
-__host__ __device__ __forceinline__ void phase_a(const int32_t* x, const uint64_t* grid, int i2, uint64_t* Y) {
+__host__ __device__ __forceinline__ void phase_a(const uint32_t* xp, const uint64_t* grid, int i2, uint64_t* Y) {
     uint64_t g[K];
 #pragma unroll
     for (int t1 = 0; t1 < K; ++t1) g[t1] = grid[(4 * t1 + S) * N2 + i2];
@@ -68,7 +70,8 @@ __host__ __device__ __forceinline__ void phase_a(const int32_t* x, const uint64_
     uint64_t v[K];
     gl::static_for<0, K>([&](auto ii) {
         constexpr int i1 = decltype(ii)::value;
-        v[gl::bitrev_c(i1, 5)] = gl::i16_mul_w128<S * i1>(x[i1]);
+        const int32_t xi = static_cast<int16_t>(static_cast<uint16_t>(i1 & 1 ? xp[i1 >> 1] >> 16 : xp[i1 >> 1]));
+        v[gl::bitrev_c(i1, 5)] = gl::i16_mul_w128<S * i1>(xi);
     });
     gl::dit_pow2<5, gl::E_W32>(v);
 #pragma unroll
@@ -102,7 +105,7 @@ __device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_
                                             uint64_t* Y, int lane) {
     constexpr int H = 1 - (S & 1);
     const int j1 = (S >> 1) * 64 + lane;
-    int32_t x[K];
+    uint32_t x[K / 2];
     size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
     load_column(w + row * cols, cols, lane, x);
     for (; row < rows; row += gridDim.x) {
