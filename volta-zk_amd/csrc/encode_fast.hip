@@ -109,10 +109,16 @@ __device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_
     size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
     load_column(w + row * cols, cols, lane, x);
     for (; row < rows; row += gridDim.x) {
+        // A SIMD holds one wave of each of two workgroups.  Phase A issues at a
+        // higher wave priority than phase B, so when both waves are ready the
+        // one heading for its workgroup's barrier goes first and the other fills
+        // its gaps (measured: 2.43 -> 2.27 ms on C3; priority 3 or 2/1 the same).
+        __builtin_amdgcn_s_setprio(1);
         phase_a<S>(x, grid, lane, Y);
         const size_t next = row + gridDim.x;
         if (next < rows) load_column(w + next * cols, cols, lane, x);
         __syncthreads();
+        __builtin_amdgcn_s_setprio(0);
         uint64_t v[32];
         phase_b<H>(Y, j1, v);
         uint64_t* o = out + row * N + j1;
