@@ -78,9 +78,10 @@ __host__ __device__ __forceinline__ void phase_a(const uint32_t* xp, const uint6
     for (int t1 = 0; t1 < K; ++t1) Y[(4 * t1 + S) * PITCH + i2] = gl::mul32x4(v[t1], g[t1]);
 }
 
-// Phase B for row j1 and output parity H: returns X[2k + H] in v[k].
+// Phase B's LDS half for row j1 and output parity H: reads Y's row and applies
+// the first radix-2 stage; the 32-point DFT over v then gives X[2k + H] in v[k].
 template <int H>
-__host__ __device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, uint64_t* v) {
+__host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1, uint64_t* v) {
     const uint64_t* y = Y + j1 * PITCH;
     gl::static_for<0, 32>([&](auto qq) {
         constexpr int q = decltype(qq)::value;
@@ -88,7 +89,6 @@ __host__ __device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, uint
         if constexpr (H == 0) v[gl::bitrev_c(q, 5)] = gl::add(a, b);
         else v[gl::bitrev_c(q, 5)] = gl::mul_pow2<gl::E_W64 * q>(gl::sub(a, b));
     });
-    gl::dit_pow2<5, gl::E_W32>(v);
 }
 
 // One wave's share of every row its workgroup owns: wave S runs phase A for
@@ -120,11 +120,15 @@ __device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_
         __syncthreads();
         __builtin_amdgcn_s_setprio(0);
         uint64_t v[32];
-        phase_b<H>(Y, j1, v);
+        phase_b_first<H>(Y, j1, v);
+        // Y is rewritten by the next row's phase A.  Once every wave holds its
+        // rows' first stage in registers the workgroup may move on, so the
+        // DFTs and stores of phase B overlap the next phase A of faster waves.
+        __syncthreads();
+        gl::dit_pow2<5, gl::E_W32>(v);
         uint64_t* o = out + row * N + j1;
 #pragma unroll
         for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * (2 * k + H));
-        __syncthreads();  // Y is rewritten by the next row's phase A
     }
 }
 
