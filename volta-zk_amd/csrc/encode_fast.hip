@@ -56,28 +56,6 @@ __device__ __forceinline__ void load_column(const int16_t* wr, size_t cols, int 
     }
 }
 
-// Phase A for coset S and column i2 of one row: writes Y[4 t1 + S][i2].
-// The four-step twiddles w_n^(i2 (4 t1 + S)) come from the L2-resident grid;
-// their loads are issued before the DFT so its arithmetic covers the latency.
-template <int S>
-__host__ __device__ __forceinline__ void phase_a(const uint32_t* xp, const uint64_t* grid, int i2, uint64_t* Y) {
-    uint64_t g[K];
-#pragma unroll
-    for (int t1 = 0; t1 < K; ++t1) g[t1] = grid[(4 * t1 + S) * N2 + i2];
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the DFT
-#endif
-    uint64_t v[K];
-    gl::static_for<0, K>([&](auto ii) {
-        constexpr int i1 = decltype(ii)::value;
-        const int32_t xi = static_cast<int16_t>(static_cast<uint16_t>(i1 & 1 ? xp[i1 >> 1] >> 16 : xp[i1 >> 1]));
-        v[gl::bitrev_c(i1, 5)] = gl::i16_mul_w128<S * i1>(xi);
-    });
-    gl::dit_pow2<5, gl::E_W32>(v);
-#pragma unroll
-    for (int t1 = 0; t1 < K; ++t1) Y[(4 * t1 + S) * PITCH + i2] = gl::mul32x4(v[t1], g[t1]);
-}
-
 // Phase B's LDS half for row j1 and output parity H: reads Y's row and applies
 // the first radix-2 stage; the 32-point DFT over v then gives X[2k + H] in v[k].
 template <int H>
@@ -91,19 +69,30 @@ __host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1
     });
 }
 
+// Coset S's pre-twiddled inputs in bit-reversed order: v[brev(i1)] = x[i1] w128^(S i1)
+// (xp: the column's 32 inputs, two i16 per word).
+template <int S>
+__device__ __forceinline__ void pretwiddle(const uint32_t* xp, uint64_t* v) {
+    gl::static_for<0, K>([&](auto ii) {
+        constexpr int i1 = decltype(ii)::value;
+        const int32_t xi = static_cast<int16_t>(static_cast<uint16_t>(i1 & 1 ? xp[i1 >> 1] >> 16 : xp[i1 >> 1]));
+        v[gl::bitrev_c(i1, 5)] = gl::i16_mul_w128<S * i1>(xi);
+    });
+}
+
 // One wave's share of every row its workgroup owns: wave S runs phase A for
 // coset S and phase B for rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and
-// parity 1 - (S & 1), so coset and parity are compile-time and no lane
-// diverges.  The even cosets (pre-twiddles are pure shifts) take the dearer
-// parity 1 (sub + shift first stage), which evens out the four waves' work
-// between the two barriers.  The workgroup walks rows blockIdx.x,
-// blockIdx.x + gridDim.x, ..., loading the next row's inputs while phase B of
-// the current row runs.
-template <int S>
-__device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_t cols, size_t rows,
+// parity H = 1 - (S & 1).  S is uniform, so no lane diverges.  Only the
+// pre-twiddles and phase B's first stage depend on the wave; the DFTs and the
+// twiddle products are one copy of code for all four waves (43 KB of code
+// instead of 136 KB).  The even cosets (pure-shift pre-twiddles) take the
+// dearer parity 1 (sub + shift first stage), which evens out the waves' work
+// per row.  The workgroup walks rows blockIdx.x, blockIdx.x + gridDim.x, ...,
+// loading the next row's inputs while phase B of the current row runs.
+__device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w, size_t cols, size_t rows,
                                             const uint64_t* __restrict__ grid, uint64_t* __restrict__ out,
                                             uint64_t* Y, int lane) {
-    constexpr int H = 1 - (S & 1);
+    const int H = 1 - (S & 1);
     const int j1 = (S >> 1) * 64 + lane;
     uint32_t x[K / 2];
     size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
@@ -114,21 +103,36 @@ __device__ __forceinline__ void encode_rows(const int16_t* __restrict__ w, size_
         // one heading for its workgroup's barrier goes first and the other fills
         // its gaps (measured: 2.43 -> 2.27 ms on C3; priority 3 or 2/1 the same).
         __builtin_amdgcn_s_setprio(1);
-        phase_a<S>(x, grid, lane, Y);
+        // Phase A: the four-step twiddles w_n^(i2 (4 t1 + S)) come from the
+        // L2-resident grid, loaded before the DFT so its arithmetic covers them.
+        uint64_t g[K];
+#pragma unroll
+        for (int t1 = 0; t1 < K; ++t1) g[t1] = grid[(4 * t1 + S) * N2 + lane];
+        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the DFT
+        uint64_t v[K];
+        switch (S) {
+            case 0: pretwiddle<0>(x, v); break;
+            case 1: pretwiddle<1>(x, v); break;
+            case 2: pretwiddle<2>(x, v); break;
+            default: pretwiddle<3>(x, v); break;
+        }
+        gl::dit_pow2<5, gl::E_W32>(v);
+#pragma unroll
+        for (int t1 = 0; t1 < K; ++t1) Y[(4 * t1 + S) * PITCH + lane] = gl::mul32x4(v[t1], g[t1]);
         const size_t next = row + gridDim.x;
         if (next < rows) load_column(w + next * cols, cols, lane, x);
         __syncthreads();
         __builtin_amdgcn_s_setprio(0);
-        uint64_t v[32];
-        phase_b_first<H>(Y, j1, v);
+        if (H == 0) phase_b_first<0>(Y, j1, v);
+        else phase_b_first<1>(Y, j1, v);
         // Y is rewritten by the next row's phase A.  Once every wave holds its
         // rows' first stage in registers the workgroup may move on, so the
         // DFTs and stores of phase B overlap the next phase A of faster waves.
         __syncthreads();
         gl::dit_pow2<5, gl::E_W32>(v);
-        uint64_t* o = out + row * N + j1;
+        uint64_t* o = out + row * N + j1 + N1 * H;
 #pragma unroll
-        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * (2 * k + H));
+        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);
     }
 }
 
@@ -137,12 +141,7 @@ __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __rest
                                                           uint64_t* __restrict__ out) {
     extern __shared__ uint64_t Y[];
     const int lane = threadIdx.x & 63;
-    switch (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) {
-        case 0: encode_rows<0>(w, cols, rows, grid, out, Y, lane); break;
-        case 1: encode_rows<1>(w, cols, rows, grid, out, Y, lane); break;
-        case 2: encode_rows<2>(w, cols, rows, grid, out, Y, lane); break;
-        default: encode_rows<3>(w, cols, rows, grid, out, Y, lane); break;
-    }
+    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, grid, out, Y, lane);
 }
 
 // grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
