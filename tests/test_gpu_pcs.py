@@ -211,6 +211,22 @@ def test_chacha8_rows_match_fpstream_and_kat(backend, oracle):
     assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 5, 4, 7, 9)).all()
 
 
+@pytest.mark.parametrize("count", [6, 8, 511, 512, 1000])
+def test_chacha8_rows_rejection_shifts_later_draws(backend, oracle, count):
+    """Rows are filled by one wave, 64 blocks (512 raw draws) per round.  On
+    the reference KAT stream the 6th raw draw of row 0 is rejected, so every
+    later value moves up by one: count 8 takes its last value from block 1,
+    count 512 from a second round; row 1 has no rejection."""
+    d = backend.chacha8_prover_secret_fp_rows_device(KAT_SEED, 0x19664BCA, 2, count)
+    got = backend.download_device(d).reshape(2, count)
+    backend.free_device(d)
+    assert (got == oracle.fp_rows(KAT_SEED, 0x19664BCA, 2, count)).all()
+    d2 = backend.chacha8_prover_secret_fp2_rows_padded_device(KAT_SEED, 0x19664BCA, 2, count // 2 + 1, count // 2 + 5)
+    got2 = backend.download_device(d2).view(np.uint64).reshape(2, count // 2 + 5, 2)
+    backend.free_device(d2)
+    assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 0x19664BCA, 2, count // 2 + 1, count // 2 + 5)).all()
+
+
 def test_chacha8_rows_large(backend, oracle):
     seed = bytes(range(32))
     d = backend.chacha8_prover_secret_fp_rows_device(seed, 1000, 513, 512)

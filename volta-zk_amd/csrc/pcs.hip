@@ -515,46 +515,73 @@ int gather_columns(Context* c, const uint64_t* m, const uint32_t* idx, uint64_t*
 }
 
 // ---- ChaCha8 FpStream rows (reference .cu:1345-1372; one stream per row) ---------------------
+//
+// A row's stream is ChaCha8 in counter mode: block k (16 words, 8 u64 draws)
+// depends only on (key, stream, k).  One wave fills one row: in each round
+// lane t makes block k0 + t, keeps its draws below p, and an exclusive scan of
+// the lanes' kept counts gives every kept draw its place in the row, exactly
+// as the sequential sampler (next_u64 in block order, rejecting draws >= p)
+// would place it.  Rounds continue until the row has `draws` kept values; a
+// rejection (probability 2^-32 per draw) only shifts later places, and may
+// take one more round.  Draw m goes to out[r * stride + m]; the lanes of a
+// round write one contiguous run.
+constexpr int CHACHA_WAVES = 4;  // rows per 256-thread workgroup
 
-__global__ void chacha8_rows_kernel(chacha8::Key key, uint64_t base_domain, size_t rows, size_t count,
-                                    uint64_t* out) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t r = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < rows; r += stride) {
-        chacha8::FpStream s(key, base_domain + r);
-        uint64_t* o = out + r * count;
-        for (size_t j = 0; j < count; ++j) o[j] = s.next_fp();
-    }
-}
-
-__global__ void chacha8_fp2_rows_kernel(chacha8::Key key, uint64_t base_domain, size_t rows, size_t count,
-                                        size_t padded, Fp2* out) {
-    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t r = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; r < rows; r += stride) {
-        chacha8::FpStream s(key, base_domain + r);
-        Fp2* o = out + r * padded;
-        for (size_t j = 0; j < count; ++j) {
-            const uint64_t a = s.next_fp();
-            const uint64_t b = s.next_fp();
-            o[j] = Fp2{a, b};
+__global__ __launch_bounds__(64 * CHACHA_WAVES) void chacha8_rows_kernel(chacha8::Key key, uint64_t base_domain,
+                                                                         size_t rows, size_t draws, size_t stride,
+                                                                         size_t zero_from, uint64_t* out) {
+    const int lane = threadIdx.x & 63;
+    const size_t row_step = static_cast<size_t>(gridDim.x) * CHACHA_WAVES;
+    for (size_t r = static_cast<size_t>(blockIdx.x) * CHACHA_WAVES + (threadIdx.x >> 6); r < rows; r += row_step) {
+        uint64_t* o = out + r * stride;
+        size_t done = 0;  // kept draws so far (uniform over the wave)
+        for (uint64_t k0 = 0; done < draws; k0 += 64) {
+            uint32_t w[16];
+            chacha8::block(key, base_domain + r, k0 + static_cast<uint64_t>(lane), w);
+            uint64_t v[8];
+            int kept = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[i] = static_cast<uint64_t>(w[2 * i]) | (static_cast<uint64_t>(w[2 * i + 1]) << 32);
+                kept += v[i] < chacha8::P ? 1 : 0;
+            }
+            int incl = kept;  // inclusive scan over the lanes
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(incl, d);
+                if (lane >= d) incl += y;
+            }
+            size_t m = done + static_cast<size_t>(incl - kept);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (v[i] < chacha8::P) {
+                    if (m < draws) o[m] = v[i];
+                    ++m;
+                }
+            }
+            done += static_cast<size_t>(__shfl(incl, 63));
         }
-        for (size_t j = count; j < padded; ++j) o[j] = Fp2{0, 0};
+        for (size_t z = zero_from + lane; z < stride; z += 64) o[z] = 0;  // Fp2 rows' padding
     }
 }
 
 int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
                     uint64_t* out) {
     const chacha8::Key key = chacha8::key_from_seed(seed);
-    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, 64, 65535)), dim3(64), 0, c->stream, key,
-                       base_domain, rows, count, out);
+    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, CHACHA_WAVES, size_t{1} << 20)),
+                       dim3(64 * CHACHA_WAVES), 0, c->stream, key, base_domain, rows, count, count, count, out);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
 
+// Fp2 rows: element j of a row is (draw 2j, draw 2j + 1); elements count ..
+// padded - 1 are zero.
 int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
                             size_t padded, Fp2* out) {
     const chacha8::Key key = chacha8::key_from_seed(seed);
-    hipLaunchKernelGGL(chacha8_fp2_rows_kernel, dim3(grid_for(rows, 64, 65535)), dim3(64), 0, c->stream, key,
-                       base_domain, rows, count, padded, out);
+    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, CHACHA_WAVES, size_t{1} << 20)),
+                       dim3(64 * CHACHA_WAVES), 0, c->stream, key, base_domain, rows, 2 * count, 2 * padded,
+                       2 * count, reinterpret_cast<uint64_t*>(out));
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
