@@ -194,6 +194,47 @@ def test_encode_of_empty_messages_is_zero(backend, n):
     assert not np.asarray(host).any()
 
 
+# The pass engine's gather reads only step-1 inputs that can be nonzero: with
+# A-point first DFTs (A = 8 at 2^13, 16 at 2^14 .. 2^17, 32 at 2^18), a message
+# of len elements needs ceil(len A / n) of them, rounded up to a compiled count
+# (1, 2, 3|4, A/4+1, 8, 16, A).  Lengths at and one past each boundary k n / A.
+ZERO_TAIL_CASES = [(13, 8, (1, 2, 3, 4, 8)), (14, 16, (1, 2, 4, 5, 8, 16)), (15, 16, (1, 2, 4, 5, 8, 16)),
+                   (17, 16, (1, 2, 4, 5, 8)), (18, 32, (1, 2, 4, 8, 9, 16))]
+
+
+@pytest.mark.parametrize("bits,a,ks", ZERO_TAIL_CASES)
+def test_encode_zero_tail_boundaries(backend, oracle, bits, a, ks):
+    n = 1 << bits
+    lens = sorted({1, n - 1, n} | {k * n // a + d for k in ks for d in (0, 1) if k * n // a + d <= n})
+    for msg_len in lens:
+        msgs = rand_fp(bits * 100003 + msg_len, (2, msg_len))
+        d = backend.upload_device(msgs.reshape(-1))
+        out = backend.ntt_fp_encode_device(d, 2, msg_len, n)
+        got = backend.download_device(out).reshape(2, n)
+        backend.free_device(d)
+        backend.free_device(out)
+        assert (got == oracle.ntt_encode_batch(msgs, n)).all(), (bits, msg_len)
+
+
+@pytest.mark.parametrize("bits,a", [(15, 16), (18, 32)])
+def test_pcs_encode_zero_tail_boundaries(backend, oracle, bits, a):
+    """The i16 weights || pads source with cols + pad at and one past k n / A,
+    the boundary falling inside the weights or inside the pads."""
+    n = 1 << bits
+    q = n // a
+    for cols, pad in [(2 * q - 3, 3), (2 * q - 3, 4), (4 * q, 1), (5 * q - 512, 512), (5 * q - 511, 512),
+                      (q // 2, q // 2), (1, 0)]:
+        g = np.random.Generator(np.random.PCG64(bits * 7919 + cols * 31 + pad))
+        w = g.integers(-(1 << 15), 1 << 15, size=2 * cols, dtype=np.int16)
+        pads = rand_fp(cols + pad, 2 * pad) if pad else np.zeros(1, np.uint64)
+        dw, dp = backend.upload_device(w), backend.upload_device(pads)
+        out = backend.pcs_encode_device(dw, 0, dp, 0, 2, cols, pad, n)
+        got = backend.download_device(out).reshape(2, n)
+        for b in (dw, dp, out):
+            backend.free_device(b)
+        assert (got == oracle.pcs_encode_i16(w, pads, 2, cols, pad, n)).all(), (bits, cols, pad)
+
+
 # ---- PCS encode of i16 message rows ---------------------------------------------------
 
 @pytest.mark.parametrize("rows,cols,pad,bits", [(5, 16, 0, 6), (9, 100, 7, 8), (17, 2048, 0, 13), (4, 2048, 512, 13),

@@ -56,6 +56,9 @@ def sample_indices(n, seed, count=48):
 @pytest.mark.parametrize("bits,length", [
     (1, 1), (1, 2), (2, 3), (3, 8), (5, 1), (7, 100), (11, 2048), (12, 4096), (12, 9),
     (13, 5000), (14, 1), (16, 65536), (17, 3), (20, 700001), (21, 1 << 21),
+    # just past k n / A, where the first pass reads k + 1 of its A step-1 inputs
+    # (A = 16 at 2^16, 8 at 2^18)
+    (16, 4097), (16, 8193), (16, 16385), (16, 20481), (18, 32769), (18, 65537), (18, 98305),
 ])
 def test_x4_ntt_matches_oracle(backend, oracle, bits, length):
     n = 1 << bits

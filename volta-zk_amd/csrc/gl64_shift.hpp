@@ -219,6 +219,43 @@ __host__ __device__ __forceinline__ void dit_pow2(uint64_t* v) {
     }
 }
 
+// The positions that may be nonzero after a stage of span LEN of dit_pow2
+// whose input may be nonzero at the positions in m: both of a pair, if either.
+constexpr uint64_t dit_mask_next(uint64_t m, int len, int n) {
+    uint64_t r = 0;
+    const int half = len / 2;
+    for (int s = 0; s < n; s += len)
+        for (int k = 0; k < half; ++k)
+            if (((m >> (s + k)) | (m >> (s + k + half))) & 1) r |= (uint64_t{1} << (s + k)) | (uint64_t{1} << (s + k + half));
+    return r;
+}
+
+// dit_pow2 for an input that is known to be zero outside the positions set in
+// MASK (bit i: v[i] may be nonzero; the other positions must hold 0).  A
+// butterfly whose second input is known zero is the copy (u, u), one whose
+// inputs are both known zero is skipped, so a zero tail of the input costs no
+// arithmetic in the stages it reaches.
+template <int LOG, int EW, uint64_t MASK, int LEN = 2>
+__host__ __device__ __forceinline__ void dit_pow2_sparse(uint64_t* v) {
+    if constexpr (LEN <= (1 << LOG)) {
+        constexpr int N = 1 << LOG;
+        constexpr int HALF = LEN / 2;
+        static_for<0, N / LEN>([&](auto g) {
+            constexpr int start = decltype(g)::value * LEN;
+            static_for<0, HALF>([&](auto kk) {
+                constexpr int k = decltype(kk)::value;
+                constexpr bool nz_u = (MASK >> (start + k)) & 1, nz_v = (MASK >> (start + k + HALF)) & 1;
+                if constexpr (nz_v) {
+                    bfly_pow2<EW * k * (N / LEN)>(v[start + k], v[start + k + HALF]);
+                } else if constexpr (nz_u) {
+                    v[start + k + HALF] = v[start + k];
+                }
+            });
+        });
+        dit_pow2_sparse<LOG, EW, dit_mask_next(MASK, LEN, N), LEN * 2>(v);
+    }
+}
+
 // Bit reversal of I over LOG bits, at compile time.
 constexpr int bitrev_c(int i, int log) {
     int r = 0;

@@ -110,6 +110,8 @@ struct SrcU64 {
     struct Raw {
         uint64_t v;
     };
+    // Inputs at index >= extent(n) are zero.
+    __host__ __device__ uint64_t extent(uint64_t n) const { return reverse || len > n ? n : len; }
     __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t nmask) const {
         return reverse ? (uint64_t{0} - idx) & nmask : idx;
     }
@@ -136,6 +138,7 @@ struct SrcMsgI16 {
         int16_t w;
         uint64_t p;
     };
+    __host__ __device__ uint64_t extent(uint64_t n) const { return cols + pad > n ? n : cols + pad; }
     __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t) const { return idx; }
     __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t, int) const {
         const uint64_t wi = idx < cols ? idx : 0;
@@ -147,12 +150,23 @@ struct SrcMsgI16 {
     }
 };
 
+// Positions of step 1's bit-reversed register array that hold ja < NZ.
+constexpr uint64_t prefix_mask(int nz, int la) {
+    uint64_t m = 0;
+    for (int ja = 0; ja < nz; ++ja) m |= uint64_t{1} << gl::bitrev_c(ja, la);
+    return m;
+}
+
 // Gather pass of row blockIdx.y of a batch: tile of 2^qb rows, inputs from
-// src, output rows n elements apart.
-template <int LA, int LB, int PL, class Src>
+// src, output rows n elements apart.  Step 1 reads only ja < NZ: the host
+// picks NZ so that every input with ja >= NZ lies in the zero tail
+// (ja B + jb >= NZ B puts the index at >= NZ n / A >= the source's extent),
+// and the A-point DFT skips the butterflies that only meet those zeros.
+template <int LA, int LB, int PL, int NZ, class Src>
 __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restrict__ y, int nb, int qb, Digits d,
                                                       const uint64_t* inner) {
     constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
+    static_assert(NZ >= 1 && NZ <= A, "step 1 reads between 1 and A inputs");
     extern __shared__ uint64_t s[];
     const uint64_t row = blockIdx.y;
     y += (row << nb) * PL;
@@ -171,19 +185,20 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
-        typename Src::Raw raw[A];
-        gl::static_for<0, A>([&](auto ja_) {
+        typename Src::Raw raw[NZ];
+        gl::static_for<0, NZ>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
             const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
             raw[ja] = src.fetch(row, idx, plane, PL);
         });
         uint64_t v[A];
-        gl::static_for<0, A>([&](auto ja_) {
+        gl::static_for<0, A>([&](auto i_) { v[decltype(i_)::value] = 0; });
+        gl::static_for<0, NZ>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
             const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
             v[gl::bitrev_c(ja, LA)] = src.finish(idx, raw[ja]);
         });
-        gl::dit_pow2<LA, ew_log<LA>()>(v);
+        gl::dit_pow2_sparse<LA, ew_log<LA>(), prefix_mask(NZ, LA)>(v);
         park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
     }
     __syncthreads();
@@ -354,16 +369,40 @@ ColFn col_for(int mode) {
     return mode == nreg::ROOT_BASE ? nreg::col_reg<LA, LB, PL, nreg::ROOT_BASE> : nullptr;
 }
 
+// The gather kernel whose step 1 reads the fewest inputs covering nza: NZ is
+// compiled for the powers of two and for A / 4 + 1, which covers a message of
+// just over a quarter of the row (cols + 512 pads at rate 1/4).
+template <int LA, int LB, int PL, class Src>
+GatherFn<Src> gather_for(uint64_t nza) {
+    constexpr int A = 1 << LA;
+    if (nza <= 1) return nreg::gather_reg<LA, LB, PL, 1, Src>;
+    if (nza <= 2) return nreg::gather_reg<LA, LB, PL, 2, Src>;
+    if constexpr (A == 8) {
+        if (nza <= 3) return nreg::gather_reg<LA, LB, PL, 3, Src>;
+        if (nza <= 4) return nreg::gather_reg<LA, LB, PL, 4, Src>;
+    } else {
+        if (nza <= 4) return nreg::gather_reg<LA, LB, PL, 4, Src>;
+        if (nza <= A / 4 + 1) return nreg::gather_reg<LA, LB, PL, A / 4 + 1, Src>;
+        if (nza <= 8) return nreg::gather_reg<LA, LB, PL, 8, Src>;
+        if constexpr (A == 32) {
+            if (nza <= 16) return nreg::gather_reg<LA, LB, PL, 16, Src>;
+        }
+    }
+    return nreg::gather_reg<LA, LB, PL, A, Src>;
+}
+
+// Kernels of a pass of radix 2^rb; nza = how many of step 1's A inputs per
+// job can be nonzero (the gather's; ignored by the column pass).
 template <int PL, class Src>
-bool kernels_for(int rb, int mode, GatherFn<Src>* g, ColFn* col) {
+bool kernels_for(int rb, int mode, uint64_t nza, GatherFn<Src>* g, ColFn* col) {
     switch (rb) {
-        case 5: *g = nreg::gather_reg<3, 2, PL, Src>; *col = col_for<3, 2, PL>(mode); break;
-        case 6: *g = nreg::gather_reg<3, 3, PL, Src>; *col = col_for<3, 3, PL>(mode); break;
-        case 7: *g = nreg::gather_reg<4, 3, PL, Src>; *col = col_for<4, 3, PL>(mode); break;
-        case 8: *g = nreg::gather_reg<4, 4, PL, Src>; *col = col_for<4, 4, PL>(mode); break;
+        case 5: *g = gather_for<3, 2, PL, Src>(nza); *col = col_for<3, 2, PL>(mode); break;
+        case 6: *g = gather_for<3, 3, PL, Src>(nza); *col = col_for<3, 3, PL>(mode); break;
+        case 7: *g = gather_for<4, 3, PL, Src>(nza); *col = col_for<4, 3, PL>(mode); break;
+        case 8: *g = gather_for<4, 4, PL, Src>(nza); *col = col_for<4, 4, PL>(mode); break;
         case 9:
             if constexpr (PL == 1) {
-                *g = nreg::gather_reg<5, 4, PL, Src>;
+                *g = gather_for<5, 4, PL, Src>(nza);
                 *col = col_for<5, 4, PL>(mode);
                 break;
             }
@@ -449,7 +488,11 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             for (int j = 0; j < d.count; ++j) d.bits[j] = r[1 + j];
             const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
             const size_t lds = tile_lds(rb, qb + PL - 1);
-            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            // step 1's input ja sits at index >= ja n / A: ja >= ceil(extent A / n) reads only zeros
+            const int la = (rb + 1) / 2;
+            const uint64_t nza = (s0.extent(uint64_t{1} << nb) + (uint64_t{1} << (nb - la)) - 1) >> (nb - la);
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), nza, &g, &col) || blocks > 0x7FFFFFFFull ||
+                lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, g, lds)) return -1;
             hipLaunchKernelGGL(g, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, s0, y,
@@ -462,7 +505,8 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             const int cb = std::min(wb, lb);
             const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
             const size_t lds = tile_lds(rb, cb + PL - 1);
-            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), &g, &col) || blocks > 0x7FFFFFFFull || lds > 160 * 1024)
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), 0, &g, &col) || blocks > 0x7FFFFFFFull ||
+                lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, col, lds)) return -1;
             hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
