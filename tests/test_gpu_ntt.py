@@ -235,6 +235,39 @@ def test_pcs_encode_zero_tail_boundaries(backend, oracle, bits, a):
         assert (got == oracle.pcs_encode_i16(w, pads, 2, cols, pad, n)).all(), (bits, cols, pad)
 
 
+def test_column_tables_and_their_fallback_agree(oracle):
+    """A column pass spanning at most 2^18 points reads its pre-twiddles from a
+    table built on first use.  Inside a coarse timing scope, where tables may
+    not grow, a pass whose table is missing builds them from the two-level
+    table instead.  Both give the oracle's transform; only the second call
+    grows device memory, by the 2^17-word table of the radix-2^9 pass."""
+    from volta_mi355x import FP2, Backend
+    rows, n = 2, 1 << 17
+    host = rand_fp(171, (rows, n))
+    with Backend(timing_policy=1) as b:
+        # an Fp2 transform of 2^17 uploads the twiddles; its passes (2^6, 2^6,
+        # 2^5) build other column tables than the Fp passes (2^9, 2^8)
+        d2 = b.upload_device(np.zeros((rows * n, 2), np.uint64), FP2)
+        o2 = b.ntt_fp2_batch_device(d2, rows, n)
+        inp = b.upload_device(host.reshape(-1))
+        outs = [b.alloc_device(rows * n, np.uint64) for _ in range(2)]
+        live = b.get_stats()["live_device_bytes"]
+        assert b.lib.volta_cuda_begin_coarse_timing(b.raw, 3) == 0
+        assert b.lib.volta_cuda_ntt_fp_batch_device(b.raw, inp.id, 0, rows, n, outs[0].id, 0) == 0
+        assert b.lib.volta_cuda_end_coarse_timing(b.raw) == 0
+        assert b.get_stats()["live_device_bytes"] == live
+        assert b.lib.volta_cuda_ntt_fp_batch_device(b.raw, inp.id, 0, rows, n, outs[1].id, 0) == 0
+        assert b.get_stats()["live_device_bytes"] == live + n * 8
+        want = oracle.ntt_forward_batch(host)
+        for o in outs:
+            assert (b.download_device(o).reshape(rows, n) == want).all()
+        assert not b.download_device(o2).view(np.uint64).any()
+        ws, res, cached = b.memory_breakdown()
+        assert ws + res + cached == b.get_stats()["live_device_bytes"]
+        for x in (d2, o2, inp, *outs):
+            b.free_device(x)
+
+
 # ---- PCS encode of i16 message rows ---------------------------------------------------
 
 @pytest.mark.parametrize("rows,cols,pad,bits", [(5, 16, 0, 6), (9, 100, 7, 8), (17, 2048, 0, 13), (4, 2048, 512, 13),

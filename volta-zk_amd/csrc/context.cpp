@@ -269,9 +269,13 @@ int ensure_grid_twiddles(Context* c, TwiddleSet* t, size_t bytes, int (*build)(C
 
 // ---- events --------------------------------------------------------------------------
 
+// Timing events only measure: nothing reads device memory on the strength of
+// their completion (downloads and pinned buffers synchronise by other means),
+// so they skip the system-scope release, which writes back and invalidates the
+// caches at every record and left ~15 us of idle GPU between primitives.
 static hipError_t ev_create(Context* c, hipEvent_t* e) {
     ++c->stats.timing_event_api_calls;
-    return hipEventCreate(e);
+    return hipEventCreateWithFlags(e, hipEventDisableSystemFence);
 }
 
 static hipError_t ev_record(Context* c, hipEvent_t e) {
@@ -742,6 +746,8 @@ VMX_API void volta_cuda_destroy(void* raw) {
             if (kv.second.grid) (void)hipFree(kv.second.grid);
             if (kv.second.split) (void)hipFree(kv.second.split);
             if (kv.second.reg) (void)hipFree(kv.second.reg);
+            for (uint64_t* t : kv.second.col)
+                if (t) (void)hipFree(t);
         }
         for (auto& p : c->pinned) {
             if (p.ready) (void)hipEventDestroy(p.ready);
@@ -940,7 +946,7 @@ VMX_API int volta_cuda_memory_breakdown(void* raw, uint64_t* workspace, uint64_t
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) w += half;
         if (kv.second.inv) w += half;
-        w += kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes;
+        w += kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes + kv.second.col_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;
@@ -1320,7 +1326,8 @@ VMX_API int volta_cuda_x4c_control_state(void* raw, RawX4cControlState* out) {
         const size_t half = std::max<size_t>(kv.first / 2, 1) * sizeof(uint64_t);
         if (kv.second.fwd) r.workspace_device_bytes += half;
         if (kv.second.inv) r.workspace_device_bytes += half;
-        r.workspace_device_bytes += kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes;
+        r.workspace_device_bytes +=
+            kv.second.grid_bytes + kv.second.split_bytes + kv.second.reg_bytes + kv.second.col_bytes;
     }
     for (const auto& b : c->resident) {
         if (!b.ptr) continue;

@@ -198,6 +198,11 @@ struct TwiddleSet {
     uint64_t* reg = nullptr;
     size_t reg_bytes = 0;
     int reg_h = 0;
+    // Pre-twiddles of the pass engine's column passes whose columns span n
+    // points (derived on the device): col[rb][i 2^(log2 n - rb) + l] = w^(i l),
+    // i < 2^rb.  col_bytes sums them.
+    uint64_t* col[16] = {};
+    size_t col_bytes = 0;
     size_t n = 0;
 };
 

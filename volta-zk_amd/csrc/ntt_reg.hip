@@ -223,10 +223,14 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
 // gets the R-point DFT over i.  For an X4 transform of 2^33 points the last
 // pass (hb = 0) meets imaginary twiddles, which mix the two coordinates: each
 // lane then also reads its partner lane's coordinate.
-template <int LA, int LB, int PL, int MODE>
+// With TBL the pre-twiddles come from ctab[(i << lb) + l] = w(n)^(H i l), a
+// table of R L words that stays in L2 (the host builds it for small R L);
+// without, from the two-level table split.
+template <int LA, int LB, int PL, int MODE, bool TBL>
 __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, int lb, int cb, const uint64_t* inner,
-                                                   const uint64_t* split, int split_h) {
+                                                   const uint64_t* split, int split_h, const uint64_t* ctab) {
     static_assert(PL == 2 || MODE == ROOT_BASE, "one-plane transforms stop at 2^31 points");
+    static_assert(!TBL || MODE == ROOT_BASE, "column tables hold real roots");
     constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
     extern __shared__ uint64_t s[];
     a += (static_cast<uint64_t>(blockIdx.y) << nb) * PL;
@@ -248,7 +252,21 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, c = PL == 2 ? (pc >> 1) : pc;
         const uint64_t l = l0 + c;
         uint64_t v[A];
-        if constexpr (MODE != ROOT_IMAG33) {
+        if constexpr (TBL) {
+            // the job's A inputs and A table words, all in flight, then A products
+            uint64_t xv[A], tv[A];
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                const uint64_t i = static_cast<uint64_t>(ja) * B + jb;
+                xv[ja] = a[PL * (base + (i << lb) + c) + plane];
+                tv[ja] = ctab[(i << lb) + l];
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            gl::static_for<0, A>([&](auto ja_) {
+                constexpr int ja = decltype(ja_)::value;
+                v[gl::bitrev_c(ja, LA)] = gl::mul32x4(xv[ja], tv[ja]);
+            });
+        } else if constexpr (MODE != ROOT_IMAG33) {
             // real roots: the pre-twiddles w^(H l (ja B + jb)) are t0 s^ja with
             // t0 = w^(H l jb) and s = w^(H l B); the job loads its A inputs and
             // four table words, then multiplies along the progression
@@ -336,6 +354,16 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
     }
 }
 
+// Column-pass table of an m = R L point column span, R = 2^rb, L = 2^lb, from
+// the two-level table of w = w(n), n = m 2^hb: out[(i << lb) + l] = w^((i l) << hb)
+// = w(m)^(i l), whatever n it is built from.
+__global__ void col_table(const uint64_t* split, int split_h, int hb, int rb, int lb, uint64_t* out) {
+    const uint64_t total = uint64_t{1} << (rb + lb), lmask = (uint64_t{1} << lb) - 1;
+    for (uint64_t j = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; j < total;
+         j += static_cast<uint64_t>(gridDim.x) * blockDim.x)
+        out[j] = tw_split(split, ((j >> lb) * (j & lmask)) << hb, split_h);
+}
+
 // Tables for the passes from the reference's table fwd = w^0 .. w^(n/2 - 1),
 // n = 2^nb >= 2^13: out = [w_4096^j, j < 2048][w^j, j < 2^h][w^(j 2^h), j < 2^(nb-h)].
 __global__ void derive_tables(const uint64_t* fwd, int nb, int h, uint64_t* out) {
@@ -358,15 +386,21 @@ namespace {
 
 template <class Src>
 using GatherFn = void (*)(Src, uint64_t*, int, int, nreg::Digits, const uint64_t*);
-using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int);
+using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int, const uint64_t*);
+
+// Column passes whose span R L is at most 2^COL_TABLE_BITS points read their
+// pre-twiddles from a table of R L words (2 MiB at most, L2-resident); larger
+// spans build them from the two-level table.
+constexpr int COL_TABLE_BITS = 18;
 
 template <int LA, int LB, int PL>
-ColFn col_for(int mode) {
+ColFn col_for(int mode, bool tbl) {
     if constexpr (PL == 2) {
-        if (mode == nreg::ROOT_NEG32) return nreg::col_reg<LA, LB, PL, nreg::ROOT_NEG32>;
-        if (mode == nreg::ROOT_IMAG33) return nreg::col_reg<LA, LB, PL, nreg::ROOT_IMAG33>;
+        if (mode == nreg::ROOT_NEG32) return nreg::col_reg<LA, LB, PL, nreg::ROOT_NEG32, false>;
+        if (mode == nreg::ROOT_IMAG33) return nreg::col_reg<LA, LB, PL, nreg::ROOT_IMAG33, false>;
     }
-    return mode == nreg::ROOT_BASE ? nreg::col_reg<LA, LB, PL, nreg::ROOT_BASE> : nullptr;
+    if (mode != nreg::ROOT_BASE) return nullptr;
+    return tbl ? nreg::col_reg<LA, LB, PL, nreg::ROOT_BASE, true> : nreg::col_reg<LA, LB, PL, nreg::ROOT_BASE, false>;
 }
 
 // The gather kernel whose step 1 reads the fewest inputs covering nza: NZ is
@@ -392,18 +426,19 @@ GatherFn<Src> gather_for(uint64_t nza) {
 }
 
 // Kernels of a pass of radix 2^rb; nza = how many of step 1's A inputs per
-// job can be nonzero (the gather's; ignored by the column pass).
+// job can be nonzero (the gather's), tbl = the column pass reads a column
+// table.
 template <int PL, class Src>
-bool kernels_for(int rb, int mode, uint64_t nza, GatherFn<Src>* g, ColFn* col) {
+bool kernels_for(int rb, int mode, uint64_t nza, bool tbl, GatherFn<Src>* g, ColFn* col) {
     switch (rb) {
-        case 5: *g = gather_for<3, 2, PL, Src>(nza); *col = col_for<3, 2, PL>(mode); break;
-        case 6: *g = gather_for<3, 3, PL, Src>(nza); *col = col_for<3, 3, PL>(mode); break;
-        case 7: *g = gather_for<4, 3, PL, Src>(nza); *col = col_for<4, 3, PL>(mode); break;
-        case 8: *g = gather_for<4, 4, PL, Src>(nza); *col = col_for<4, 4, PL>(mode); break;
+        case 5: *g = gather_for<3, 2, PL, Src>(nza); *col = col_for<3, 2, PL>(mode, tbl); break;
+        case 6: *g = gather_for<3, 3, PL, Src>(nza); *col = col_for<3, 3, PL>(mode, tbl); break;
+        case 7: *g = gather_for<4, 3, PL, Src>(nza); *col = col_for<4, 3, PL>(mode, tbl); break;
+        case 8: *g = gather_for<4, 4, PL, Src>(nza); *col = col_for<4, 4, PL>(mode, tbl); break;
         case 9:
             if constexpr (PL == 1) {
                 *g = gather_for<5, 4, PL, Src>(nza);
-                *col = col_for<5, 4, PL>(mode);
+                *col = col_for<5, 4, PL>(mode, tbl);
                 break;
             }
             return false;
@@ -465,6 +500,32 @@ int derive_reg_tables(Context* c, TwiddleSet* t) {
     return 0;
 }
 
+// The column table of a pass spanning 2^(rb + lb) points, built from this
+// transform's two-level table on first use and kept with the other tables of
+// that size.  Inside a coarse timing scope, where tables may not grow, a
+// missing table leaves *out null and the pass builds its pre-twiddles itself.
+static int col_table_for(Context* c, const RegTables& tb, int hb, int rb, int lb, const uint64_t** out) {
+    TwiddleSet& t = c->twiddles[size_t{1} << (rb + lb)];
+    t.n = size_t{1} << (rb + lb);
+    if (!t.col[rb]) {
+        if (c->coarse_active) return 0;
+        const size_t bytes = (size_t{1} << (rb + lb)) * sizeof(uint64_t);
+        void* p = nullptr;
+        VMX_HIP(c, hipMalloc(&p, bytes));
+        ++c->stats.allocation_calls;
+        c->stats.live_device_bytes += bytes;
+        c->stats.peak_device_bytes = std::max(c->stats.peak_device_bytes, c->stats.live_device_bytes);
+        t.col[rb] = static_cast<uint64_t*>(p);
+        t.col_bytes += bytes;
+        const unsigned blocks = static_cast<unsigned>(std::min<size_t>((size_t{1} << (rb + lb)) / 256, 4096));
+        hipLaunchKernelGGL(nreg::col_table, dim3(std::max(blocks, 1u)), dim3(256), 0, c->stream, tb.split,
+                           tb.split_h, hb, rb, lb, t.col[rb]);
+        VMX_HIP(c, hipGetLastError());
+    }
+    *out = t.col[rb];
+    return 0;
+}
+
 // The passes of rows transforms with inputs from src; shift(src, r0) moves
 // src to row r0 for each launch slice of at most 65535 rows.
 template <int PL, class Src, class Shift>
@@ -491,7 +552,7 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             // step 1's input ja sits at index >= ja n / A: ja >= ceil(extent A / n) reads only zeros
             const int la = (rb + 1) / 2;
             const uint64_t nza = (s0.extent(uint64_t{1} << nb) + (uint64_t{1} << (nb - la)) - 1) >> (nb - la);
-            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), nza, &g, &col) || blocks > 0x7FFFFFFFull ||
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), nza, false, &g, &col) || blocks > 0x7FFFFFFFull ||
                 lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, g, lds)) return -1;
@@ -505,12 +566,16 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             const int cb = std::min(wb, lb);
             const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
             const size_t lds = tile_lds(rb, cb + PL - 1);
-            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), 0, &g, &col) || blocks > 0x7FFFFFFFull ||
-                lds > 160 * 1024)
+            const uint64_t* ctab = nullptr;
+            if (nreg::root_mode(nb) == nreg::ROOT_BASE && rb + lb <= COL_TABLE_BITS &&
+                col_table_for(c, tb, hb, rb, lb, &ctab))
+                return -1;
+            if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), 0, ctab != nullptr, &g, &col) ||
+                blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, col, lds)) return -1;
             hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
-                               nb, hb, lb, cb, tb.inner, tb.split, tb.split_h);
+                               nb, hb, lb, cb, tb.inner, tb.split, tb.split_h, ctab);
             VMX_HIP(c, hipGetLastError());
             lbits += rb;
         }
