@@ -28,7 +28,9 @@
 //   step 2: one thread takes the B values of one (coordinate, column, ka),
 //     DFTs them over jb and stores Y[ka + A kb] straight to HBM.
 // LDS holds (coordinate, column) pairs fastest, then jb, then ka with a pitch
-// of PW (B + 1) words, so both steps' accesses avoid bank conflicts.
+// of PW (B + 1) words (column passes) or PW B + 32 / A words (the gather,
+// whose step 2 takes ka fastest so that its stores cover whole lines), so
+// both steps' accesses avoid bank conflicts.
 //
 // Elements are PL u64 wide (PL = 1: Fp; PL = 2: Fp2, coordinate p of element e
 // at 2 e + p); each coordinate is transformed independently, except that the
@@ -172,7 +174,11 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     y += (row << nb) * PL;
     const int pwb = qb + (PL - 1);  // (coordinate, row) pairs: 2^pwb
     const uint32_t PW = 1u << pwb;
-    const uint32_t pitch = PW * (B + 1);
+    // Step 2 runs ka fastest, so each store writes A adjacent outputs of a row
+    // (whole 128-byte lines for A = 16).  Its LDS reads, (pc, ka) at
+    // pc + ka pitch, then meet distinct banks in every 32-lane group when
+    // pitch = 32 / A (mod 32) words; step 1's writes are contiguous per ka.
+    const uint32_t pitch = PW * B + 32 / A;
     uint64_t nat0, row0;
     int mid_bits;
     gather_tile(nb, RB, qb, d, nat0, row0, mid_bits);
@@ -204,7 +210,7 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     __syncthreads();
     __builtin_amdgcn_s_setprio(0);
     for (uint32_t job = threadIdx.x; job < (PW << LA); job += THREADS) {
-        const uint32_t pc = job & (PW - 1), ka = job >> pwb;
+        const uint32_t ka = job & (A - 1), pc = job >> LA;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
         uint64_t v[B];
         unpark<LB>(s, v, pc, ka, PW, pitch);
@@ -456,10 +462,16 @@ int plan(int nb, int planes, int* r) {
     return passes;
 }
 
-// LDS bytes of a tile: 2^pwb (coordinate, column) pairs x A x (B + 1) words.
+// LDS bytes of a column tile: 2^pwb (coordinate, column) pairs x A x (B + 1) words.
 size_t tile_lds(int rb, int pwb) {
     const size_t A = size_t{1} << ((rb + 1) / 2), B = size_t{1} << (rb / 2);
     return (size_t{1} << pwb) * A * (B + 1) * sizeof(uint64_t);
+}
+
+// LDS bytes of a gather tile: A rows of 2^pwb B words, each padded by 32 / A.
+size_t gather_lds(int rb, int pwb) {
+    const size_t A = size_t{1} << ((rb + 1) / 2), B = size_t{1} << (rb / 2);
+    return (((size_t{1} << pwb) * B) * A + 32) * sizeof(uint64_t);
 }
 
 template <class K>
@@ -548,7 +560,7 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             d.count = passes - 2;
             for (int j = 0; j < d.count; ++j) d.bits[j] = r[1 + j];
             const uint64_t blocks = uint64_t{1} << (nb - rb - qb);
-            const size_t lds = tile_lds(rb, qb + PL - 1);
+            const size_t lds = gather_lds(rb, qb + PL - 1);
             // step 1's input ja sits at index >= ja n / A: ja >= ceil(extent A / n) reads only zeros
             const int la = (rb + 1) / 2;
             const uint64_t nza = (s0.extent(uint64_t{1} << nb) + (uint64_t{1} << (nb - la)) - 1) >> (nb - la);
