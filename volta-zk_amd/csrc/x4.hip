@@ -123,9 +123,44 @@ __global__ __launch_bounds__(THREADS) void direct_fold(const u64x2* __restrict__
 
 // ---- Moebius transform -------------------------------------------------------------------
 
+// LDS word of tile index i: one word of padding per 16 keeps the rounds below
+// free of bank conflicts (a round's lanes step by 1, 17 or 272 words).
+__device__ __forceinline__ uint32_t mob_slot(uint32_t i) { return i + (i >> 4); }
+
+// One round of the Moebius transform on the tile in LDS: bits [b, b + K) of
+// the middle index, all K of them in registers.  Group g takes the 2^K
+// elements of one (plane-column, the other bits of i); the bits' updates
+// commute, so any grouping of the bits gives the same result.
+template <int K>
+__device__ __forceinline__ void mobius_round(uint64_t* s, int b, int rb, uint32_t planecols, int inverse) {
+    const uint32_t lo_mask = (1u << b) - 1, hi_bits = static_cast<uint32_t>(rb - b - K);
+    const uint32_t groups = planecols << (rb - K);
+    for (uint32_t g = threadIdx.x; g < groups; g += THREADS) {
+        const uint32_t lo = g & lo_mask, hi = (g >> b) & ((1u << hi_bits) - 1), pc = g >> (rb - K);
+        const uint32_t i0 = (pc << rb) + lo + (hi << (b + K));
+        uint64_t v[1 << K];
+        gl::static_for<0, (1 << K)>([&](auto m_) {
+            constexpr int m = decltype(m_)::value;
+            v[m] = s[mob_slot(i0 + (static_cast<uint32_t>(m) << b))];
+        });
+        gl::static_for<0, K>([&](auto j_) {
+            constexpr int j = decltype(j_)::value;
+            gl::static_for<0, (1 << K)>([&](auto m_) {
+                constexpr int m = decltype(m_)::value;
+                if constexpr ((m >> j) & 1) v[m] = inverse ? gl::add(v[m], v[m ^ (1 << j)]) : gl::sub(v[m], v[m ^ (1 << j)]);
+            });
+        });
+        gl::static_for<0, (1 << K)>([&](auto m_) {
+            constexpr int m = decltype(m_)::value;
+            s[mob_slot(i0 + (static_cast<uint32_t>(m) << b))] = v[m];
+        });
+    }
+}
+
 // One pass over the middle index of [H][R][L] (R = 2^rb, L = 2^lb): for every
 // bit of i, the element with the bit set gains (inverse) or loses the one
-// without.  Workgroup (h, l0) takes C = 2^cb adjacent columns.
+// without.  Workgroup (h, l0) takes C = 2^cb adjacent columns; the bits are
+// applied up to four at a time in registers, with the tile in LDS in between.
 __global__ __launch_bounds__(THREADS) void mobius_pass(u64x2* a, int rb, int lb, int cb, int inverse) {
     extern __shared__ uint64_t s[];
     const uint32_t C = 1u << cb;
@@ -137,26 +172,22 @@ __global__ __launch_bounds__(THREADS) void mobius_pass(u64x2* a, int rb, int lb,
     for (uint32_t e = threadIdx.x; e < CR; e += THREADS) {
         const uint32_t i = e >> cb, c = e & (C - 1);
         const u64x2 v = a[base + (static_cast<uint64_t>(i) << lb) + c];
-        s[(c << rb) + i] = v.x;
-        s[CR + (c << rb) + i] = v.y;
+        s[mob_slot((c << rb) + i)] = v.x;
+        s[mob_slot(CR + (c << rb) + i)] = v.y;
     }
     __syncthreads();
-    const uint32_t pairs = CR;  // (2 planes x C x R) / 2
-    for (int b = 0; b < rb; ++b) {
-        const uint32_t bit = 1u << b;
-        for (uint32_t e = threadIdx.x; e < pairs; e += THREADS) {
-            // e enumerates (plane-column, i with bit b clear)
-            const uint32_t col = e >> (rb - 1), r = e & ((1u << (rb - 1)) - 1);
-            const uint32_t lo = ((r >> b) << (b + 1)) | (r & (bit - 1));
-            const uint32_t base_s = col << rb;
-            const uint64_t x = s[base_s + lo], y = s[base_s + (lo | bit)];
-            s[base_s + (lo | bit)] = inverse ? gl::add(y, x) : gl::sub(y, x);
+    for (int b = 0; b < rb; b += 4) {
+        switch (rb - b >= 4 ? 4 : rb - b) {
+            case 4: mobius_round<4>(s, b, rb, 2 * C, inverse); break;
+            case 3: mobius_round<3>(s, b, rb, 2 * C, inverse); break;
+            case 2: mobius_round<2>(s, b, rb, 2 * C, inverse); break;
+            default: mobius_round<1>(s, b, rb, 2 * C, inverse); break;
         }
         __syncthreads();
     }
     for (uint32_t e = threadIdx.x; e < CR; e += THREADS) {
         const uint32_t i = e >> cb, c = e & (C - 1);
-        a[base + (static_cast<uint64_t>(i) << lb) + c] = u64x2{s[(c << rb) + i], s[CR + (c << rb) + i]};
+        a[base + (static_cast<uint64_t>(i) << lb) + c] = u64x2{s[mob_slot((c << rb) + i)], s[mob_slot(CR + (c << rb) + i)]};
     }
 }
 
@@ -275,7 +306,8 @@ int fp2_mobius(Context* c, gl::Fp2* values, uint64_t n, bool inverse) {
         const int cb = std::min(MOBIUS_RUN_BITS, lb);
         const int rb = std::min(nb - done, TILE_BITS - cb);
         const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
-        const size_t lds = size_t{16} << (rb + cb);
+        const size_t words = size_t{2} << (rb + cb);  // two planes
+        const size_t lds = (words + (words >> 4) + 1) * sizeof(uint64_t);  // + the slots' padding
         if (blocks > 0x7FFFFFFFull) return fail_msg(c, "Moebius pass exceeds its launch limits");
         if (set_lds(c, mobius_pass, lds)) return -1;
         hipLaunchKernelGGL(mobius_pass, dim3(static_cast<unsigned>(blocks)), dim3(THREADS), lds, c->stream, a, rb,
