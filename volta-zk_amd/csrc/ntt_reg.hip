@@ -38,6 +38,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "context.hpp"
 #include "gl64.hpp"
@@ -231,10 +232,13 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
 // lane then also reads its partner lane's coordinate.
 // With TBL the pre-twiddles come from ctab[(i << lb) + l] = w(n)^(H i l), a
 // table of R L words that stays in L2 (the host builds it for small R L);
-// without, from the two-level table split.
+// without, from the two-level table split, and then every output is also
+// multiplied by scale (one product per job, on t0): the inverse transform's
+// n^-1 when this is its last pass.
 template <int LA, int LB, int PL, int MODE, bool TBL>
 __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, int lb, int cb, const uint64_t* inner,
-                                                   const uint64_t* split, int split_h, const uint64_t* ctab) {
+                                                   const uint64_t* split, int split_h, const uint64_t* ctab,
+                                                   uint64_t scale) {
     static_assert(PL == 2 || MODE == ROOT_BASE, "one-plane transforms stop at 2^31 points");
     static_assert(!TBL || MODE == ROOT_BASE, "column tables hold real roots");
     constexpr int A = 1 << LA, B = 1 << LB, RB = LA + LB;
@@ -289,6 +293,7 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
             __builtin_amdgcn_sched_barrier(0);  // every load of the job is in flight before the arithmetic
             uint64_t t = gl::mul32x4(p0, q0);
             uint64_t st = gl::mul32x4(p1, q1);
+            if (scale != 1) t = gl::mul32x4(t, scale);
             if constexpr (MODE == ROOT_NEG32) {  // w(2^32)^e = (-1)^e b_32^e
                 if (e0 & 1) t = gl::neg(t);
                 if (es & 1) st = gl::neg(st);
@@ -392,7 +397,8 @@ namespace {
 
 template <class Src>
 using GatherFn = void (*)(Src, uint64_t*, int, int, nreg::Digits, const uint64_t*);
-using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int, const uint64_t*);
+using ColFn = void (*)(uint64_t*, int, int, int, int, const uint64_t*, const uint64_t*, int, const uint64_t*,
+                      uint64_t);
 
 // Column passes whose span R L is at most 2^COL_TABLE_BITS points read their
 // pre-twiddles from a table of R L words (2 MiB at most, L2-resident); larger
@@ -545,6 +551,17 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
     int r[nreg::MAX_PASSES] = {};
     const int passes = plan(nb, PL, r);
     if (passes == 0) return fail_msg(c, "NTT size outside the pass engine's range");
+    // A scaled source (the inverse transform's n^-1) hands its scale to the
+    // last column pass when that pass builds its pre-twiddles as a progression
+    // (span n > 2^COL_TABLE_BITS, real roots): one product per job instead of
+    // one per input.
+    uint64_t last_scale = 1;
+    if constexpr (std::is_same<Src, nreg::SrcU64>::value) {
+        if (src.scale != 1 && passes >= 2 && nb > COL_TABLE_BITS && nreg::root_mode(nb) == nreg::ROOT_BASE) {
+            last_scale = src.scale;
+            src.scale = 1;
+        }
+    }
     const int wb = nreg::run_bits(nb, PL);
     GatherFn<Src> g = nullptr;
     ColFn col = nullptr;
@@ -586,8 +603,9 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
                 blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");
             if (allow_lds(c, col, lds)) return -1;
+            const uint64_t pass_scale = p == 0 && ctab == nullptr ? last_scale : uint64_t{1};
             hipLaunchKernelGGL(col, dim3(static_cast<unsigned>(blocks), cnt), dim3(nreg::THREADS), lds, c->stream, y,
-                               nb, hb, lb, cb, tb.inner, tb.split, tb.split_h, ctab);
+                               nb, hb, lb, cb, tb.inner, tb.split, tb.split_h, ctab, pass_scale);
             VMX_HIP(c, hipGetLastError());
             lbits += rb;
         }
