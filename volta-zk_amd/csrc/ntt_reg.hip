@@ -71,16 +71,28 @@ __device__ __forceinline__ uint64_t partner(uint64_t v) {
     return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
+// The R = A B inner twiddles w_R^(jb ka) of a tile, at ptw[jb A + ka] in LDS:
+// filled once per workgroup (R <= 512 words, two per thread at most) so that
+// step 1 reads each with one LDS load instead of an index, a table load and a
+// sign select.  The caller synchronises before the first park().
+template <int LA, int LB>
+__device__ __forceinline__ void fill_park_twiddles(uint64_t* ptw, const uint64_t* inner) {
+    constexpr int A = 1 << LA, RB = LA + LB;
+    for (uint32_t i = threadIdx.x; i < (1u << RB); i += THREADS)
+        ptw[i] = inner_pow(inner, ((i >> LA) * (i & (A - 1))) << (GBITS - RB));
+}
+
 // Step 1's tail: v (natural order over ka after the A-point DFT) times
 // w_R^(jb ka), parked at (pc, jb, ka).
 template <int LA, int LB>
 __device__ __forceinline__ void park(uint64_t* s, const uint64_t* v, uint32_t pc, uint32_t jb, uint32_t PW,
-                                     uint32_t pitch, const uint64_t* inner) {
-    constexpr int A = 1 << LA, RB = LA + LB;
+                                     uint32_t pitch, const uint64_t* ptw) {
+    constexpr int A = 1 << LA;
     s[pc + PW * jb] = v[0];
+    const uint64_t* row = ptw + jb * A;
     gl::static_for<1, A>([&](auto ka_) {
         constexpr int ka = decltype(ka_)::value;
-        s[pc + PW * jb + ka * pitch] = gl::mul32x4(v[ka], inner_pow(inner, (jb * ka) << (GBITS - RB)));
+        s[pc + PW * jb + ka * pitch] = gl::mul32x4(v[ka], row[ka]);
     });
 }
 
@@ -180,6 +192,9 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     // pc + ka pitch, then meet distinct banks in every 32-lane group when
     // pitch = 32 / A (mod 32) words; step 1's writes are contiguous per ka.
     const uint32_t pitch = PW * B + 32 / A;
+    uint64_t* ptw = s + A * pitch;  // the inner twiddles follow the tile
+    fill_park_twiddles<LA, LB>(ptw, inner);
+    __syncthreads();
     uint64_t nat0, row0;
     int mid_bits;
     gather_tile(nb, RB, qb, d, nat0, row0, mid_bits);
@@ -206,7 +221,7 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
             v[gl::bitrev_c(ja, LA)] = src.finish(idx, raw[ja]);
         });
         gl::dit_pow2_sparse<LA, ew_log<LA>(), prefix_mask(NZ, LA)>(v);
-        park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
+        park<LA, LB>(s, v, pc, jb, PW, pitch, ptw);
     }
     __syncthreads();
     __builtin_amdgcn_s_setprio(0);
@@ -247,6 +262,9 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
     const int pwb = cb + (PL - 1);
     const uint32_t PW = 1u << pwb;
     const uint32_t pitch = PW * (B + 1);
+    uint64_t* ptw = s + A * pitch;  // the inner twiddles follow the tile
+    fill_park_twiddles<LA, LB>(ptw, inner);
+    __syncthreads();
     const uint64_t lblocks = (uint64_t{1} << lb) >> cb;
     const uint64_t blk = tile_id();
     const uint64_t h = blk / lblocks;
@@ -349,7 +367,7 @@ __global__ __launch_bounds__(THREADS) void col_reg(uint64_t* a, int nb, int hb, 
             });
         }
         gl::dit_pow2<LA, ew_log<LA>()>(v);
-        park<LA, LB>(s, v, pc, jb, PW, pitch, inner);
+        park<LA, LB>(s, v, pc, jb, PW, pitch, ptw);
     }
     __syncthreads();
     __builtin_amdgcn_s_setprio(0);
@@ -468,16 +486,18 @@ int plan(int nb, int planes, int* r) {
     return passes;
 }
 
-// LDS bytes of a column tile: 2^pwb (coordinate, column) pairs x A x (B + 1) words.
+// LDS bytes of a column tile: 2^pwb (coordinate, column) pairs x A x (B + 1)
+// words, then the R = A B inner twiddles.
 size_t tile_lds(int rb, int pwb) {
     const size_t A = size_t{1} << ((rb + 1) / 2), B = size_t{1} << (rb / 2);
-    return (size_t{1} << pwb) * A * (B + 1) * sizeof(uint64_t);
+    return ((size_t{1} << pwb) * A * (B + 1) + A * B) * sizeof(uint64_t);
 }
 
-// LDS bytes of a gather tile: A rows of 2^pwb B words, each padded by 32 / A.
+// LDS bytes of a gather tile: A rows of 2^pwb B words, each padded by 32 / A,
+// then the R = A B inner twiddles.
 size_t gather_lds(int rb, int pwb) {
     const size_t A = size_t{1} << ((rb + 1) / 2), B = size_t{1} << (rb / 2);
-    return (((size_t{1} << pwb) * B) * A + 32) * sizeof(uint64_t);
+    return (((size_t{1} << pwb) * B) * A + 32 + A * B) * sizeof(uint64_t);
 }
 
 template <class K>
