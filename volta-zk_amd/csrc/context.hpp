@@ -165,10 +165,9 @@ enum WorkspaceSlot : int {
     WS_AUX0 = 2,
     WS_AUX1 = 3,
     WS_PARTIALS = 4,  // combination partial sums
-    WS_TRANSPOSE = 5, // four-step intermediate
-    WS_AUX2 = 6,      // combination coefficient sums
-    WS_HASH = 7,      // Merkle column-group chaining values
-    WS_COUNT = 8,
+    WS_AUX2 = 5,      // combination coefficient sums
+    WS_HASH = 6,      // Merkle column-group chaining values
+    WS_COUNT = 7,
 };
 
 struct TimingRecord {

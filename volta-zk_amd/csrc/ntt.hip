@@ -6,15 +6,11 @@
 //
 // Rows of n >= 2^13 (u64, Fp2, and i16 weights + pads message rows) run on the
 // pass engine of ntt_reg.hip (register four-steps with shift-only sub-DFTs).
-// The generic paths below serve smaller rows (any power-of-two n):
-//   * n <= 2^14: one workgroup per row, the whole row in LDS (<= 128 KiB of the
-//     160 KiB per CU), bit-reversed load then radix-2^2 DIT passes (two stages
-//     per LDS round trip).  One HBM read + one HBM write per element.
-//   * n  > 2^14: four-step split n = n1*n2.  Pass A: n1-point column DFTs of
-//     C adjacent columns per workgroup plus the w^(i2*k1) twiddle; pass B:
-//     n2-point row DFTs of R adjacent rows with a transposed, R-element
-//     coalesced store.  Two HBM round trips.
-// All twiddles come from the reference's table w^0..w^(n/2-1): a stage of
+// The generic path below serves smaller rows (any power-of-two n <= 2^14): one
+// workgroup per row, the whole row in LDS (<= 128 KiB of the 160 KiB per CU),
+// bit-reversed load then radix-2^2 DIT passes (two stages per LDS round trip).
+// One HBM read + one HBM write per element.
+// Its twiddles come from the reference's table w^0..w^(n/2-1): a stage of
 // length L of any sub-transform uses tw[k * n/L], and w^e for e >= n/2 is
 // -tw[e - n/2].
 #include <hip/hip_runtime.h>
@@ -95,64 +91,6 @@ __global__ __launch_bounds__(512) void ntt_row_lds(Load ld, Store st, int bits, 
     }
 }
 
-// ---- four-step passes ---------------------------------------------------------------
-
-// Pass A: for columns i2 in [cb*C, cb*C + C) of row `row`, the n1-point DFT over
-// i1 of x[n2*i1 + i2], times w^(i2*k1), stored at y[k1*n2 + i2].
-template <class Load>
-__global__ __launch_bounds__(512) void ntt4_pass_a(Load ld, uint64_t* y, int bits, int b1, int cbits,
-                                                  const uint64_t* tw) {
-    extern __shared__ uint64_t s[];
-    const size_t n = size_t{1} << bits;
-    const size_t n1 = size_t{1} << b1;
-    const size_t n2 = n >> b1;
-    const size_t C = size_t{1} << cbits;
-    const size_t blocks_per_row = n2 >> cbits;
-    const size_t row = blockIdx.x / blocks_per_row;
-    const size_t c0 = (blockIdx.x - row * blocks_per_row) << cbits;
-    for (size_t e = threadIdx.x; e < C * n1; e += blockDim.x) {
-        const size_t i1 = e >> cbits, c = e & (C - 1);
-        s[c * n1 + brev(static_cast<uint32_t>(i1), b1)] = ld(row, n2 * i1 + c0 + c);
-    }
-    __syncthreads();
-    lds_dit(s, static_cast<int>(C), b1, bits, tw);
-    const size_t half = n >> 1;
-    for (size_t e = threadIdx.x; e < C * n1; e += blockDim.x) {
-        const size_t k1 = e >> cbits, c = e & (C - 1);
-        const size_t i2 = c0 + c;
-        const uint64_t v = gl::mul(s[c * n1 + k1], tw_pow(tw, (i2 * k1) & (n - 1), half));
-        y[row * n + k1 * n2 + i2] = v;
-    }
-}
-
-// Pass B: for k1 in [rb*R, rb*R + R), the n2-point DFT over i2 of y[k1*n2 + i2],
-// stored at out[k1 + n1*k2] (times `scale`).
-template <class Store>
-__global__ __launch_bounds__(512) void ntt4_pass_b(const uint64_t* y, Store st, int bits, int b1, int rbits,
-                                                  const uint64_t* tw, uint64_t scale) {
-    extern __shared__ uint64_t s[];
-    const size_t n = size_t{1} << bits;
-    const size_t n1 = size_t{1} << b1;
-    const int b2 = bits - b1;
-    const size_t n2 = n >> b1;
-    const size_t R = size_t{1} << rbits;
-    const size_t blocks_per_row = n1 >> rbits;
-    const size_t row = blockIdx.x / blocks_per_row;
-    const size_t r0 = (blockIdx.x - row * blocks_per_row) << rbits;
-    for (size_t e = threadIdx.x; e < R * n2; e += blockDim.x) {
-        const size_t r = e >> b2, i2 = e & (n2 - 1);
-        s[r * n2 + brev(static_cast<uint32_t>(i2), b2)] = y[row * n + (r0 + r) * n2 + i2];
-    }
-    __syncthreads();
-    lds_dit(s, static_cast<int>(R), b2, bits, tw);
-    for (size_t e = threadIdx.x; e < R * n2; e += blockDim.x) {
-        const size_t k2 = e >> rbits, r = e & (R - 1);
-        uint64_t v = s[r * n2 + k2];
-        if (scale != 1) v = gl::mul(v, scale);
-        st(row * n + (r0 + r) + n1 * k2, v);
-    }
-}
-
 // ---- launchers -------------------------------------------------------------------------
 
 // Row-offset adjusters so a launch can start at row r0.
@@ -206,40 +144,9 @@ static int run_ntt(Context* c, Load ld, Store st, size_t rows, size_t n, const u
         }
         return 0;
     }
-    // Four-step through the transpose workspace, a bounded number of rows at a time.
-    const int b1 = (bits + 1) / 2;
-    const int b2 = bits - b1;
-    if (b1 > LDS_MAX_BITS) return fail_msg(c, "NTT size exceeds the supported maximum of 2^28");
-    const int cbits = std::min(b2, LDS_MAX_BITS - b1);
-    const int rbits = std::min(b1, LDS_MAX_BITS - b2);
-    const size_t row_bytes = n * sizeof(uint64_t);
-    const size_t max_ws = size_t{1} << 31;  // 2 GiB of intermediate at most
-    const size_t chunk = std::max<size_t>(1, std::min(rows, max_ws / row_bytes));
-    if (ensure_ws(c, WS_TRANSPOSE, chunk * row_bytes)) return -1;
-    uint64_t* y = ws<uint64_t>(c, WS_TRANSPOSE);
-    auto ka = ntt4_pass_a<Load>;
-    auto kb = ntt4_pass_b<Store>;
-    const size_t lds_a = (size_t{1} << (b1 + cbits)) * sizeof(uint64_t);
-    const size_t lds_b = (size_t{1} << (b2 + rbits)) * sizeof(uint64_t);
-    VMX_HIP(c, allow_lds(ka, lds_a));
-    VMX_HIP(c, allow_lds(kb, lds_b));
-    const size_t blocks_a = size_t{1} << (b2 - cbits);
-    const size_t blocks_b = size_t{1} << (b1 - rbits);
-    const int ta = static_cast<int>(std::min<size_t>(512, std::max<size_t>(64, (size_t{1} << (b1 + cbits)) / 4)));
-    const int tb = static_cast<int>(std::min<size_t>(512, std::max<size_t>(64, (size_t{1} << (b2 + rbits)) / 4)));
-    for (size_t r0 = 0; r0 < rows; r0 += chunk) {
-        const size_t cnt = std::min(chunk, rows - r0);
-        Load l2 = ld;
-        Store s2 = st;
-        shift_rows(l2, s2, r0, n);
-        hipLaunchKernelGGL(ka, dim3(static_cast<unsigned>(cnt * blocks_a)), dim3(ta), lds_a, c->stream, l2, y,
-                           bits, b1, cbits, tw);
-        VMX_HIP(c, hipGetLastError());
-        hipLaunchKernelGGL(kb, dim3(static_cast<unsigned>(cnt * blocks_b)), dim3(tb), lds_b, c->stream,
-                           static_cast<const uint64_t*>(y), s2, bits, b1, rbits, tw, scale);
-        VMX_HIP(c, hipGetLastError());
-    }
-    return 0;
+    // Rows above 2^LDS_MAX_BITS points run on the pass engine (ntt_reg.hip), whose
+    // tables every size from 2^13 to 2^31 gets with its twiddles.
+    return fail_msg(c, "NTT rows above 2^14 points need the pass engine's tables");
 }
 
 static RegTables reg_tables(const TwiddleSet* t) {
