@@ -116,6 +116,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "vo_merkle_tree": (None, [vp, sz, vp]),
         "vo_merkle_paths": (None, [vp, sz, vp, sz, vp]),
         "vo_merkle_bench_matrix": (None, [sz, sz, vp, i32]),
+        "vo_commit_root": (i32, [vp, sz, sz, sz, sz, vp, vp, vp, vp, i32]),
         "vo_fp2_pow": (Fp2C, [Fp2C, u64]),
         "vo_fp2_inv": (Fp2C, [Fp2C]),
         "vo_x4_root_of_unity": (Fp2C, [ctypes.c_uint32]),
@@ -447,6 +448,28 @@ def merkle_bench_matrix(rows: int, cols: int, threads: int | None = None) -> np.
     out = np.zeros(rows * cols, np.uint64)
     lib().vo_merkle_bench_matrix(rows, cols, _ptr(out), threads or default_threads())
     return out
+
+
+def commit_root(w: np.ndarray, rows: int, cols: int, pad: int, code_len: int, seed: bytes,
+                threads: int | None = None, keep: bool = False):
+    """The CPU commit (commit_impl, rust/volta-pcs/src/ligero.rs:543-624): pads,
+    messages, per-row NTT, blake3 column leaves and the Merkle root.  Returns
+    the 32-byte root, or (root, encoded rows x code_len, pads rows x pad) with
+    ``keep``."""
+    w = np.ascontiguousarray(w, dtype=np.int16).reshape(-1)
+    assert w.size == rows * cols
+    s = _seed(seed)
+    root = np.zeros(32, np.uint8)
+    enc = np.zeros((rows, code_len), np.uint64) if keep else None
+    pads = np.zeros((rows, max(pad, 1)), np.uint64) if keep else None
+    rc = lib().vo_commit_root(_ptr(w), rows, cols, pad, code_len, _ptr(s), _ptr(root),
+                              _ptr(enc) if keep else None, _ptr(pads) if keep else None,
+                              threads or default_threads())
+    if rc != 0:
+        raise ValueError("invalid commit geometry")
+    if keep:
+        return root.tobytes(), enc, pads[:, :pad]
+    return root.tobytes()
 
 
 # ---- X4 extension-field transforms (volta_oracle_x4.c) ----------------------------------

@@ -257,25 +257,43 @@ void vo_pcs_encode_i16(const int16_t* w, const uint64_t* pads, size_t rows, size
     free(tw);
 }
 
-/* Column-parallel (each task owns a column range and walks every row once),
- * like the reference's data-block pass (ligero.rs:694-709); field sums are
- * exact, so the split does not change the result. */
+/* combine_rows (ligero.rs:680-720) for any number of coefficient rows: the
+ * data block is split into threads*4 column chunks, each task walks every
+ * row once over its chunk and accumulates all combinations (the reference
+ * fuses u_q and u_c the same way); the pad block (rows x pad) is summed
+ * serially afterwards.  combine_row_range (ligero.rs:1114-1135) gives the
+ * same sums: field addition is exact, so the order does not matter. */
 void vo_pcs_combine_rows(const int16_t* w, const uint64_t* pads, const vo_fp2* coeffs,
                          size_t rows, size_t cols, size_t pad, size_t combinations,
                          vo_fp2* out, int threads) {
-    size_t msg_len = cols + pad;
-#pragma omp parallel for schedule(static) num_threads(threads)
-    for (size_t j = 0; j < msg_len; ++j) {
-        for (size_t c = 0; c < combinations; ++c) {
-            vo_fp2 acc = {0, 0};
-            for (size_t i = 0; i < rows; ++i) {
-                uint64_t x = j < cols ? vo_fp_from_i64((int64_t)w[i * cols + j])
-                                      : pads[i * pad + (j - cols)];
-                acc = vo_fp2_add(acc, vo_fp2_mul_base(coeffs[c * rows + i], x));
+    const size_t msg_len = cols + pad;
+    for (size_t k = 0; k < combinations * msg_len; ++k) out[k] = (vo_fp2){0, 0};
+    const size_t n_chunks = (size_t)(threads > 0 ? threads : 1) * 4;
+    const size_t chunk = (cols + n_chunks - 1) / n_chunks;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+    for (size_t ci = 0; ci < n_chunks; ++ci) {
+        const size_t j0 = ci * chunk;
+        if (j0 >= cols) continue;
+        const size_t len = cols - j0 < chunk ? cols - j0 : chunk;
+        for (size_t i = 0; i < rows; ++i) {
+            const int16_t* row = w + i * cols + j0;
+            for (size_t dj = 0; dj < len; ++dj) {
+                const uint64_t x = vo_fp_from_i64((int64_t)row[dj]);
+                for (size_t c = 0; c < combinations; ++c) {
+                    vo_fp2* u = out + c * msg_len + j0 + dj;
+                    *u = vo_fp2_add(*u, vo_fp2_mul_base(coeffs[c * rows + i], x));
+                }
             }
-            out[c * msg_len + j] = acc;
         }
     }
+    for (size_t i = 0; i < rows; ++i)
+        for (size_t q = 0; q < pad; ++q) {
+            const uint64_t x = pads[i * pad + q];
+            for (size_t c = 0; c < combinations; ++c) {
+                vo_fp2* u = out + c * msg_len + cols + q;
+                *u = vo_fp2_add(*u, vo_fp2_mul_base(coeffs[c * rows + i], x));
+            }
+        }
 }
 
 void vo_combine_rows_fp(const uint64_t* msgs, const vo_fp2* coeffs, size_t rows, size_t cols,

@@ -65,8 +65,10 @@ void vo_pcs_messages(const int16_t* w, const uint64_t* pads, size_t rows, size_t
 /* commit_impl encode step: messages + NttPlan::forward per row (ligero.rs:584-592) */
 void vo_pcs_encode_i16(const int16_t* w, const uint64_t* pads, size_t rows, size_t cols,
                        size_t pad, size_t code_len, uint64_t* out, int threads);
-/* u[c][j] = sum_i coeffs[c*rows+i] * msg_i[j] over message rows lift(w)||pads
- * (combine_row_range ligero.rs:1114-1135; coefficient layout lib.rs:6522-6569). */
+/* u[c][j] = sum_i coeffs[c*rows+i] * msg_i[j] over message rows lift(w)||pads,
+ * with combine_rows' loop order (ligero.rs:680-720: column chunks, each walking
+ * all rows once, all combinations fused; the pad block after); the sums equal
+ * combine_row_range's (ligero.rs:1114-1135).  Coefficient layout lib.rs:6522-6569. */
 void vo_pcs_combine_rows(const int16_t* w, const uint64_t* pads, const vo_fp2* coeffs,
                          size_t rows, size_t cols, size_t pad, size_t combinations,
                          vo_fp2* out, int threads);
@@ -133,6 +135,11 @@ void vo_merkle_tree(const uint8_t* leaves, size_t n, uint8_t* tree);         /* 
 void vo_merkle_paths(const uint8_t* tree, size_t leaves, const uint32_t* idx, size_t queries,
                      uint8_t* paths);                                          /* merkle.rs:43-51 */
 void vo_merkle_bench_matrix(size_t rows, size_t cols, uint64_t* m, int threads); /* p7_blake3_merkle.cu:243 */
+/* commit_impl (ligero.rs:543-624) composed: pads -> messages -> per-row NTT ->
+ * column leaves -> Merkle root.  encoded/pads may be NULL. */
+int vo_commit_root(const int16_t* w, size_t rows, size_t cols, size_t pad, size_t code_len,
+                   const uint8_t seed[32], uint8_t root[32], uint64_t* encoded, uint64_t* pads,
+                   int threads);
 
 /* ---- X4 extension-field transforms (volta_oracle_x4.c) -------------------
  * rust/volta-pcs/src/x4/ntt.rs; cuda/volta_x4b.cuh. */

@@ -204,3 +204,36 @@ void vo_merkle_bench_matrix(size_t rows, size_t cols, uint64_t* m, int threads) 
 #pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
     for (long i = 0; i < (long)(rows * cols); ++i) m[i] = ((uint64_t)i * 0x9E3779B9ull + 17) % p;
 }
+
+/* commit_impl (ligero.rs:543-624) end to end, without a backend: per-row pads
+ * FpStream::domain_separated(seed, r) (ligero.rs:555-563), each row encoded
+ * as NttPlan::forward of lift(w) || pads || 0 (ligero.rs:584-592), blake3
+ * column leaves (ligero.rs:596-616) and MerkleTree::from_leaves (ligero.rs:620);
+ * writes the 32-byte root.  `encoded` (rows x code_len) and `pads` (rows x pad)
+ * receive the intermediate matrices when non-null.  Returns 0, or -1 when the
+ * geometry is invalid (code_len not a power of two, cols + pad > code_len) or
+ * memory runs out. */
+int vo_commit_root(const int16_t* w, size_t rows, size_t cols, size_t pad, size_t code_len,
+                   const uint8_t seed[32], uint8_t root[32], uint64_t* encoded, uint64_t* pads,
+                   int threads) {
+    if (!rows || !cols || code_len < 1 || (code_len & (code_len - 1)) || cols + pad > code_len) return -1;
+    uint64_t* enc = encoded ? encoded : (uint64_t*)malloc(rows * code_len * sizeof(uint64_t));
+    uint64_t* pd = pads ? pads : (uint64_t*)malloc((rows * pad + 1) * sizeof(uint64_t));
+    uint8_t* leaves = (uint8_t*)malloc(code_len * 32);
+    uint8_t* tree = (uint8_t*)malloc((2 * code_len - 1) * 32);
+    int rc = 0;
+    if (!enc || !pd || !leaves || !tree) {
+        rc = -1;
+    } else {
+        if (pad) vo_fp_rows(seed, 0, rows, pad, pd, threads);
+        vo_pcs_encode_i16(w, pd, rows, cols, pad, code_len, enc, threads);
+        vo_hash_fp_columns(enc, rows, code_len, leaves, threads);
+        vo_merkle_tree(leaves, code_len, tree);
+        memcpy(root, tree + 32 * (2 * code_len - 2), 32);
+    }
+    if (!encoded) free(enc);
+    if (!pads) free(pd);
+    free(leaves);
+    free(tree);
+    return rc;
+}

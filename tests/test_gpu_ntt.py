@@ -167,6 +167,68 @@ def test_fp2_batch_device_componentwise(backend, oracle):
         assert (got[:, :, comp] == oracle.ntt_forward_batch(host[:, :, comp].copy())).all()
 
 
+@pytest.mark.parametrize("bits,rows", [(13, 3), (14, 2), (15, 4), (16, 2), (17, 3), (18, 2)])
+def test_fp2_batch_device_random_rows_pass_engine(backend, oracle, bits, rows):
+    """The opening's mask transform (ntt_fp2_batch_device at the code length,
+    mask rows = claims + 1 > 1): random Fp2 rows on the pass engine, rows
+    after the first reached through the batch offset, with an element offset
+    on both sides."""
+    from volta_mi355x import FP2
+    n = 1 << bits
+    host = rand_fp(bits * 31 + rows, (rows, n, 2))
+    host[0, :2] = [[P - 1, P - 1], [0, 1]]
+    inp = backend.alloc_device(rows * n + 3, FP2)
+    backend.upload_into(inp, 3, host.reshape(-1))
+    out = backend.alloc_device(rows * n + 5, FP2)
+    backend._check(backend.lib.volta_cuda_ntt_fp2_batch_device(backend.raw, inp.id, 3, rows, n, out.id, 5))
+    got = backend.download_device(out, 5, rows * n).view(np.uint64).reshape(rows, n, 2)
+    kept = backend.download_device(inp, 3, rows * n).view(np.uint64).reshape(rows, n, 2)
+    for b in (inp, out):
+        backend.free_device(b)
+    assert (kept == host).all()  # out of place: the input is preserved
+    for comp in (0, 1):
+        assert (got[:, :, comp] == oracle.ntt_forward_batch(host[:, :, comp].copy())).all(), comp
+
+
+@pytest.mark.parametrize("bits", [6, 12, 13, 16])
+def test_overlapping_ntt_regions_are_rejected(backend, bits):
+    """The resident transforms are out of place (the input is preserved,
+    .cu:6545-6579): any overlap of input and output, exact aliasing
+    included, is an error and leaves the buffer untouched."""
+    from volta_mi355x import FP2
+    lib, raw = backend.lib, backend.raw
+    n = 1 << bits
+    host = rand_fp(bits, 2 * n + 8)
+    buf = backend.upload_device(host)
+    for call in (lib.volta_cuda_ntt_fp_batch_device, lib.volta_mi355x_ntt_fp_inverse_batch_device):
+        for in_off, out_off in ((0, 0), (0, n // 2 + 1), (8, 0), (n, n)):
+            assert call(raw, buf.id, in_off, 1, n, buf.id, out_off) != 0, (in_off, out_off)
+            assert "overlap" in backend.last_error()
+    assert lib.volta_cuda_ntt_fp_batch_device(raw, buf.id, 0, 1, n, buf.id, n) == 0  # adjacent: fine
+    f2 = backend.alloc_device(2 * n, FP2)
+    assert lib.volta_cuda_ntt_fp2_batch_device(raw, f2.id, 0, 1, n, f2.id, 0) != 0
+    assert "overlap" in backend.last_error()
+    assert (backend.download_device(buf)[:n] == host[:n]).all()
+    backend.free_device(buf)
+    backend.free_device(f2)
+
+
+def test_base_field_sizes_above_the_two_adicity_are_rejected(backend):
+    """p - 1 = 2^32 (2^32 - 1): base-field roots exist up to 2^32 points; the
+    reference's twiddle table for 2^32 would be 16 GiB.  Sizes above 2^31 are
+    refused before any table is built or uploaded."""
+    lib, raw = backend.lib, backend.raw
+    buf = backend.alloc_device(8, np.uint64)
+    before = backend.get_stats()["h2d_bytes"]
+    live = backend.get_stats()["live_device_bytes"]
+    for n in (1 << 32, 1 << 33):
+        assert lib.volta_cuda_ntt_fp_batch_device(raw, buf.id, 0, 1, n, buf.id, 0) != 0
+        assert "geometry" in backend.last_error() or "size" in backend.last_error()
+    assert backend.get_stats()["h2d_bytes"] == before
+    assert backend.get_stats()["live_device_bytes"] == live
+    backend.free_device(buf)
+
+
 def test_compact_encode_device(backend, oracle):
     for rows, msg_len, bits in [(7, 100, 9), (4, 4096, 14), (3, 1000, 16)]:
         n = 1 << bits

@@ -23,6 +23,12 @@ namespace {
 
 bool pow2(size_t n) { return n >= 2 && (n & (n - 1)) == 0; }
 
+// Base-field transforms: p - 1 = 2^32 (2^32 - 1) bounds the root order at
+// 2^32, and a 2^32-point twiddle table alone would be 16 GiB; sizes above
+// 2^31 are refused as invalid geometry before any table is built.
+constexpr size_t MAX_BASE_NTT = size_t{1} << 31;
+bool base_ntt_size(size_t n) { return pow2(n) && n <= MAX_BASE_NTT; }
+
 template <class F>
 int guarded(Context* c, const char* what, F&& f) noexcept {
     try {
@@ -61,14 +67,14 @@ int resident_ntt(Context* c, const uint64_t* in, size_t in_stride, size_t msg_le
 VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows, size_t n,
                                               uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident Fp NTT geometry");
+    if (!c || !rows || !base_ntt_size(n)) return fail_msg(c, "invalid resident Fp NTT geometry");
     return guarded(c, "resident Fp NTT", [&] {
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp NTT geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
         if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
             return -1;
-        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident Fp NTT input and output overlap");
         return resident_ntt(c, static_cast<const uint64_t*>(in), n, n, rows, n, static_cast<uint64_t*>(out),
                             false);
@@ -80,14 +86,14 @@ VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_
 VMX_API int volta_cuda_ntt_fp2_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows, size_t n,
                                                uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident Fp2 NTT geometry");
+    if (!c || !rows || !base_ntt_size(n)) return fail_msg(c, "invalid resident Fp2 NTT geometry");
     return guarded(c, "resident Fp2 NTT", [&] {
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp2 NTT geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
         if (region_elems(c, in_id, in_off, total, 16, &in) || region_elems(c, out_id, out_off, total, 16, &out))
             return -1;
-        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident Fp2 NTT input and output overlap");
         uint64_t h2d = 0;
         TwiddleSet* t = nullptr;
@@ -129,7 +135,7 @@ int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size
 // Replaces volta_cuda_ntt_fp (.cu:5534-5544).
 VMX_API int volta_cuda_ntt_fp(void* raw, const uint64_t* msg, size_t msg_len, size_t n, uint64_t* out) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !msg || !out || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT geometry");
+    if (!c || !msg || !out || !base_ntt_size(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT geometry");
     return guarded(c, "Fp NTT", [&] { return host_ntt(c, msg, 1, msg_len, n, out); });
 }
 
@@ -137,14 +143,14 @@ VMX_API int volta_cuda_ntt_fp(void* raw, const uint64_t* msg, size_t msg_len, si
 VMX_API int volta_cuda_ntt_fp_batch(void* raw, const uint64_t* msgs, size_t rows, size_t msg_len, size_t n,
                                        uint64_t* out) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !msgs || !out || !rows || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT batch geometry");
+    if (!c || !msgs || !out || !rows || !base_ntt_size(n) || msg_len > n) return fail_msg(c, "invalid Fp NTT batch geometry");
     return guarded(c, "Fp NTT batch", [&] { return host_ntt(c, msgs, rows, msg_len, n, out); });
 }
 
 // Replaces volta_cuda_ntt_fp2 (.cu:5561-5571).
 VMX_API int volta_cuda_ntt_fp2(void* raw, const Fp2* msg, size_t msg_len, size_t n, Fp2* out) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !msg || !out || !pow2(n) || msg_len > n) return fail_msg(c, "invalid Fp2 NTT geometry");
+    if (!c || !msg || !out || !base_ntt_size(n) || msg_len > n) return fail_msg(c, "invalid Fp2 NTT geometry");
     return guarded(c, "Fp2 NTT", [&] {
         const size_t bytes = n * sizeof(Fp2), in_bytes = msg_len * sizeof(Fp2);
         if (ensure_ws(c, WS_IN, bytes) || ensure_ws(c, WS_OUT, bytes)) return -1;
@@ -412,14 +418,14 @@ VMX_API int volta_cuda_chacha8_prover_secret_fp2_rows_padded_device(void* raw, u
 VMX_API int volta_mi355x_ntt_fp_inverse_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows,
                                                         size_t n, uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !rows || !pow2(n)) return fail_msg(c, "invalid resident inverse Fp NTT geometry");
+    if (!c || !rows || !base_ntt_size(n)) return fail_msg(c, "invalid resident inverse Fp NTT geometry");
     return guarded(c, "resident inverse Fp NTT", [&] {
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident inverse Fp NTT geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
         if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
             return -1;
-        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total && in != out)
+        if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident inverse Fp NTT input and output overlap");
         return resident_ntt(c, static_cast<const uint64_t*>(in), n, n, rows, n, static_cast<uint64_t*>(out), true);
     });
@@ -431,7 +437,7 @@ VMX_API int volta_mi355x_ntt_fp_inverse_batch_device(void* raw, uint64_t in_id, 
 VMX_API int volta_mi355x_ntt_fp_encode_device(void* raw, uint64_t in_id, size_t in_off, size_t rows,
                                                  size_t msg_len, size_t n, uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !rows || !pow2(n) || msg_len > n) return fail_msg(c, "invalid resident Fp encode geometry");
+    if (!c || !rows || !base_ntt_size(n) || msg_len > n) return fail_msg(c, "invalid resident Fp encode geometry");
     return guarded(c, "resident Fp encode", [&] {
         size_t in_n = 0, out_n = 0;
         if (!mul_ok(rows, msg_len, &in_n) || !mul_ok(rows, n, &out_n))
@@ -454,7 +460,7 @@ VMX_API int volta_mi355x_pcs_encode_device(void* raw, uint64_t w_id, size_t w_of
                                               size_t pads_off, size_t rows, size_t cols, size_t pad, size_t code_len,
                                               uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
-    if (!c || !rows || !cols || !pow2(code_len) || cols + pad > code_len || cols + pad < cols)
+    if (!c || !rows || !cols || !base_ntt_size(code_len) || cols + pad > code_len || cols + pad < cols)
         return fail_msg(c, "invalid resident PCS encode geometry");
     return guarded(c, "resident PCS encode", [&] {
         size_t wn = 0, pn = 0, on = 0;

@@ -1,6 +1,8 @@
-// abi_stubs.cpp -- the volta_cuda_* symbols outside the Ligero encode /
-// row-combination path (GEMM and fixed-point inference, LogUp, X4b/X4c,
-// sumcheck helpers, BLAKE3/Merkle).  The reference's Rust loader resolves all
+// abi_stubs.cpp -- the volta_cuda_* symbols outside the Ligero commit path
+// (GEMM and fixed-point inference, LogUp rounds and trees, the X4b keyed
+// trees and the X4c arena/session machinery, sumcheck helpers).  The Ligero
+// encode, combinations, opening helpers, BLAKE3/Merkle trees and X4
+// transforms are implemented in abi_pcs.cpp.  The reference's Rust loader resolves all
 // of them eagerly (rust/volta-accel/src/cuda.rs:1159-1449), so each is
 // exported with its exact signature; calling one fails explicitly with a
 // last_error message and never falls back to host computation.

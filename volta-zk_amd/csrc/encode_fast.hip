@@ -168,13 +168,11 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
         return 1;
     if (rows == 0) return 0;
     if (ensure_grid_twiddles(c, t, size_t{enc13::N1} * enc13::N2 * sizeof(uint64_t), enc13::build_grid)) return -1;
-    static bool lds_ok = false;  // the attribute is per-process, per-kernel
-    if (!lds_ok) {
-        VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(enc13::encode13_i16),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(enc13::LDS_BYTES)));
-        lds_ok = true;
-    }
+    // The LDS limit is an attribute of the kernel on the current device: set
+    // it on every call (a host-side call of about a microsecond), so no flag
+    // shared between contexts, threads or devices is needed.
+    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(enc13::encode13_i16),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(enc13::LDS_BYTES)));
     // Two workgroups fit a CU (LDS); a persistent grid of that many overlaps
     // each row's input loads with the previous row's phase B.
     const size_t per_cu = 2;

@@ -575,9 +575,16 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
     // last column pass when that pass builds its pre-twiddles as a progression
     // (span n > 2^COL_TABLE_BITS, real roots): one product per job instead of
     // one per input.
+    // Column passes whose columns span at most 2^COL_TABLE_BITS points (real
+    // roots only) read a column table; the last pass spans all n points.  The
+    // same predicate decides the hand-off below and the table lookup of each
+    // pass, and the last pass refuses a table while it holds the scale.
+    auto table_span = [&](int span_bits) {
+        return nreg::root_mode(nb) == nreg::ROOT_BASE && span_bits <= COL_TABLE_BITS;
+    };
     uint64_t last_scale = 1;
     if constexpr (std::is_same<Src, nreg::SrcU64>::value) {
-        if (src.scale != 1 && passes >= 2 && nb > COL_TABLE_BITS && nreg::root_mode(nb) == nreg::ROOT_BASE) {
+        if (src.scale != 1 && passes >= 2 && nreg::root_mode(nb) == nreg::ROOT_BASE && !table_span(nb)) {
             last_scale = src.scale;
             src.scale = 1;
         }
@@ -616,9 +623,9 @@ int run_passes(Context* c, const RegTables& tb, Src src, Shift shift, uint64_t* 
             const uint64_t blocks = uint64_t{1} << (nb - rb - cb);
             const size_t lds = tile_lds(rb, cb + PL - 1);
             const uint64_t* ctab = nullptr;
-            if (nreg::root_mode(nb) == nreg::ROOT_BASE && rb + lb <= COL_TABLE_BITS &&
-                col_table_for(c, tb, hb, rb, lb, &ctab))
-                return -1;
+            if (table_span(rb + lb) && col_table_for(c, tb, hb, rb, lb, &ctab)) return -1;
+            if (p == 0 && last_scale != 1 && ctab != nullptr)
+                return fail_msg(c, "inverse NTT scale handed to a column pass that reads a table");
             if (!kernels_for<PL, Src>(rb, nreg::root_mode(nb), 0, ctab != nullptr, &g, &col) ||
                 blocks > 0x7FFFFFFFull || lds > 160 * 1024)
                 return fail_msg(c, "NTT pass exceeds its launch limits");

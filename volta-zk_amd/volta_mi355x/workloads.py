@@ -1,8 +1,10 @@
 """Synthetic inputs for the five benchmark configurations.
 
 The generators are this build's choice (the configurations name only the
-distributions); each is deterministic and its output is fingerprinted in
-tests/golden so drift is caught.
+distributions); each is deterministic, and tests/golden/config_inputs.json
+holds a SHA-256 fingerprint plus the first and last elements of every
+configuration's packed input (checked by tests/test_config_fixtures.py), so
+a change of generator or of numpy's streams is caught.
 
 C1  256 rows x 2^12 uniform Fp -> 2^14 (rate 1/4); rows from
     FpStream::domain_separated(SEED_C1, row) (device ChaCha8, the reference's
