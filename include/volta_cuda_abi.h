@@ -361,6 +361,19 @@ int volta_mi355x_pcs_encode_device(void* ctx, uint64_t w_id, size_t w_off, uint6
                                    size_t rows, size_t cols, size_t pad, size_t code_len, uint64_t out_id,
                                    size_t out_off);
 
+/* volta_cuda_pcs_combine_rows_device without any allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * partial sums live in a fixed 16 MiB device array per GPU (held until the
+ * process ends); a combination whose partials need more is refused with an
+ * error (C3's two combinations need 8 MiB).  All calls on one GPU share the
+ * array: calls that overlap in time on one GPU race.  Same arguments,
+ * results and RawStats as volta_cuda_pcs_combine_rows_device. */
+int volta_mi355x_pcs_combine_rows_device_noalloc(void* ctx, uint64_t w_id, size_t w_off, uint64_t pads_id,
+                                                 size_t pads_off, uint64_t coeffs_id, size_t coeffs_off, size_t rows,
+                                                 size_t cols, size_t pad, size_t combinations, uint64_t out_id,
+                                                 size_t out_off);
+
 /* out[c][j] = sum_i coeffs[c*rows + i] * m[i*cols + j] over dense u64 (Fp)
  * rows; output combinations x cols VoltaFp2.  The reference's own arithmetic
  * benchmark combines u64 rows (cuda/p7_pcs_arithmetic.cu:275-288). */

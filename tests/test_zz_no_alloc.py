@@ -1,0 +1,77 @@
+"""The allocation-free combination entry point
+(volta_mi355x_pcs_combine_rows_device_noalloc) against the allocating one
+(volta_cuda_pcs_combine_rows_device) and the oracle, through the C ABI.
+
+Two calls in a row, the second smaller, so the second runs over scratch the
+first left behind; neither call may allocate (RawStats allocation_calls and
+live_device_bytes unchanged); a plan beyond the fixed scratch is refused."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+P = 0xFFFF_FFFF_0000_0001
+
+
+def rand_i16(seed, size):
+    return np.random.Generator(np.random.PCG64(seed)).integers(-(1 << 15), 1 << 15, size=size, dtype=np.int16)
+
+
+def rand_fp(seed, shape):
+    return np.random.Generator(np.random.PCG64(seed)).integers(0, P, size=shape, dtype=np.uint64)
+
+
+def call(b, name, w, dp, dc, rows, cols, pad, comb, out):
+    fn = getattr(b.lib, name)
+    return fn(b.raw, w.id, 0, dp.id, 0, dc.id, 0, rows, cols, pad, comb, out.id, 0)
+
+
+@pytest.mark.parametrize("shapes", [[(4096, 2048, 512, 2), (300, 100, 7, 3)],
+                                    [(1 << 16, 2048, 0, 2), (5, 3, 1, 1)]])
+def test_noalloc_combination_matches_allocating_entry_point(oracle, shapes):
+    from volta_mi355x import FP2, Backend
+    with Backend() as b:
+        for k, (rows, cols, pad, comb) in enumerate(shapes):
+            w = rand_i16(rows + k, rows * cols)
+            pads = rand_fp(rows * 3 + k, rows * pad) if pad else np.zeros(1, np.uint64)
+            co = rand_fp(comb + k, (comb * rows, 2))
+            dw, dp = b.upload_device(w), b.upload_device(pads)
+            dc = b.upload_device(co, FP2)
+            ref_out = b.alloc_device(comb * (cols + pad), FP2)
+            out = b.alloc_device(comb * (cols + pad), FP2)
+            assert call(b, "volta_cuda_pcs_combine_rows_device", dw, dp, dc, rows, cols, pad, comb, ref_out) == 0
+            b.synchronize()
+            before = b.get_stats()
+            assert call(b, "volta_mi355x_pcs_combine_rows_device_noalloc", dw, dp, dc, rows, cols, pad, comb,
+                        out) == 0, b.last_error()
+            b.synchronize()
+            after = b.get_stats()
+            assert after["allocation_calls"] == before["allocation_calls"]
+            assert after["live_device_bytes"] == before["live_device_bytes"]
+            assert after["calls"]["pcs_rows"] == before["calls"]["pcs_rows"] + 1
+            got = b.download_device(out).view(np.uint64).reshape(comb, cols + pad, 2)
+            want = b.download_device(ref_out).view(np.uint64).reshape(comb, cols + pad, 2)
+            for x in (dw, dp, dc, ref_out, out):
+                b.free_device(x)
+            assert (got == want).all(), (rows, cols, pad, comb)
+            if rows * cols <= 4096 * 2048:
+                assert (got == oracle.pcs_combine_rows(w, pads if pad else None, co, rows, cols, pad, comb)).all()
+
+
+def test_noalloc_combination_refuses_plans_beyond_its_scratch():
+    """2^17 rows of 2048 columns split into 256 partial chunks: two
+    combinations need 16 MiB of partials plus their sums, more than the
+    fixed array; the call fails with an error and writes nothing."""
+    from volta_mi355x import FP2, Backend
+    rows, cols, comb = 1 << 17, 2048, 2
+    with Backend() as b:
+        dw = b.alloc_device(rows * cols, np.int16)
+        dp = b.alloc_device(1, np.uint64)
+        dc = b.alloc_device(comb * rows, FP2)
+        out = b.alloc_device(comb * cols, FP2)
+        b.zero_device(out, 0, comb * cols)
+        assert call(b, "volta_mi355x_pcs_combine_rows_device_noalloc", dw, dp, dc, rows, cols, 0, comb, out) != 0
+        assert "scratch" in b.last_error() and "16777216" in b.last_error()
+        assert not b.download_device(out).view(np.uint64).any()
+        for x in (dw, dp, dc, out):
+            b.free_device(x)

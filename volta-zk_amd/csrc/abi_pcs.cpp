@@ -200,7 +200,7 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
 namespace {
 int combine_device(Context* c, uint64_t w_id, size_t w_off, uint64_t pads_id, size_t pads_off, uint64_t co_id,
                    size_t co_off, size_t rows, size_t cols, size_t pad, size_t combinations, uint64_t out_id,
-                   size_t out_off) {
+                   size_t out_off, bool noalloc = false) {
     size_t wn = 0, pn = 0, cn = 0, msg_len = 0, on = 0;
     if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(combinations, rows, &cn) ||
         !add_ok(cols, pad, &msg_len) || !mul_ok(combinations, msg_len, &on))
@@ -210,8 +210,9 @@ int combine_device(Context* c, uint64_t w_id, size_t w_off, uint64_t pads_id, si
         region_elems(c, co_id, co_off, cn, 16, &co) || region_elems(c, out_id, out_off, on, 16, &out))
         return -1;
     if (begin_op(c) || mark_op(c, 1)) return -1;
-    if (pcs_combine_rows(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
-                         static_cast<const Fp2*>(co), rows, cols, pad, combinations, static_cast<Fp2*>(out)))
+    const auto combine = noalloc ? pcs_combine_rows_noalloc : pcs_combine_rows;
+    if (combine(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), static_cast<const Fp2*>(co),
+                rows, cols, pad, combinations, static_cast<Fp2*>(out)))
         return -1;
     if (mark_op(c, 2)) return -1;
     return finish_op(c, OP_PCS_ROWS, 0, 0);
@@ -228,6 +229,25 @@ VMX_API int volta_cuda_pcs_combine_rows_device(void* raw, uint64_t w_id, size_t 
     return guarded(c, "resident PCS combination", [&] {
         return combine_device(c, w_id, w_off, pads_id, pads_off, co_id, co_off, rows, cols, pad, combinations,
                               out_id, out_off);
+    });
+}
+
+// volta_cuda_pcs_combine_rows_device without allocation, for callers that
+// cannot allocate (code under HIP graph capture, serving loops): the partials
+// and coefficient sums live in a fixed 16 MiB device array per GPU instead of
+// the context's grow-only workspaces, and a plan that needs more is refused
+// with an error.  All calls on one GPU share that array, so calls that overlap
+// in time on one GPU (several contexts or threads) race; each call rewrites
+// every scratch word it reads.  Same arguments, results and stats.
+VMX_API int volta_mi355x_pcs_combine_rows_device_noalloc(void* raw, uint64_t w_id, size_t w_off, uint64_t pads_id,
+                                                          size_t pads_off, uint64_t co_id, size_t co_off, size_t rows,
+                                                          size_t cols, size_t pad, size_t combinations,
+                                                          uint64_t out_id, size_t out_off) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !rows || !cols || !combinations) return fail_msg(c, "invalid resident PCS combination geometry");
+    return guarded(c, "allocation-free resident PCS combination", [&] {
+        return combine_device(c, w_id, w_off, pads_id, pads_off, co_id, co_off, rows, cols, pad, combinations,
+                              out_id, out_off, true);
     });
 }
 

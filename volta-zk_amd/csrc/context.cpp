@@ -9,6 +9,7 @@
 // Every entry point returns 0 on success and -1 (or a HIP status) on failure
 // with a message for volta_cuda_last_error; nothing throws across the ABI.
 #include "context.hpp"
+#include "kernels.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -725,6 +726,9 @@ VMX_API int volta_cuda_create(void** out) {
         c->timing_mode = TIMING_HOST_BARRIER_WALL;
     }
     c->stats.timing_mode = c->timing_mode;
+    // Resolve this device's scratch array of the allocation-free combination.
+    // A failure only disables that entry point, which then reports it.
+    (void)combine_scratch_attach(c);
     return 0;
     VMX_GUARD_END(c, "context construction")
 }

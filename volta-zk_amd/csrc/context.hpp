@@ -238,6 +238,10 @@ struct Context {
     std::chrono::steady_clock::time_point phase_start{};
     uint64_t phase_ns[3]{};
     uint32_t inject_no_write = 0;
+    // this device's address of the allocation-free combination's scratch
+    // array (null when it could not be resolved)
+    void* scratch = nullptr;
+    std::string scratch_error;
     std::string error;
 };
 

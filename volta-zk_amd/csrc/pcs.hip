@@ -3,6 +3,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "chacha8.hpp"
@@ -327,26 +330,40 @@ static size_t comb_chunk(size_t rows, size_t col_blocks, size_t largest = COMB_C
     return chunk;
 }
 
-int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
-                     size_t cols, size_t pad, size_t combinations, Fp2* out) {
-    const size_t msg_len = cols + pad;
-    const size_t col_blocks = (cols + CI_TILE - 1) / CI_TILE;
-    const size_t chunk = comb_chunk(rows, col_blocks, CI_CHUNK);
-    const size_t chunks = (rows + chunk - 1) / chunk;
-    size_t per_chunk = 0, bytes = 0, sum_bytes = 0;
-    if (!mul_ok(combinations, msg_len, &per_chunk) || !mul_ok(per_chunk * sizeof(Fp2), chunks, &bytes) ||
-        !mul_ok(chunks * combinations, 2 * sizeof(uint64_t), &sum_bytes))
+// The i16 combination's launch plan: rows per partial chunk and the bytes of
+// the per-chunk partials (none for one chunk: it writes out directly) and of
+// the chunks' coefficient sums.
+struct CombinePlan {
+    size_t msg_len, col_blocks, chunk, chunks, per_chunk, part_bytes, sum_bytes;
+};
+
+static int combine_plan(Context* c, size_t rows, size_t cols, size_t pad, size_t combinations, CombinePlan* p) {
+    p->msg_len = cols + pad;
+    p->col_blocks = (cols + CI_TILE - 1) / CI_TILE;
+    p->chunk = comb_chunk(rows, p->col_blocks, CI_CHUNK);
+    p->chunks = (rows + p->chunk - 1) / p->chunk;
+    size_t bytes = 0;
+    if (!mul_ok(combinations, p->msg_len, &p->per_chunk) || !mul_ok(p->per_chunk * sizeof(Fp2), p->chunks, &bytes) ||
+        !mul_ok(p->chunks * combinations, 2 * sizeof(uint64_t), &p->sum_bytes))
         return fail_msg(c, "PCS combination partials overflow size_t");
-    if (chunks > 65535 || combinations > 65535)
+    if (p->chunks > 65535 || combinations > 65535)
         return fail_msg(c, "PCS combination row or combination count exceeds the supported maximum");
-    // one chunk: the partials are the result, written straight into out
-    if ((chunks > 1 && ensure_ws(c, WS_PARTIALS, bytes)) || ensure_ws(c, WS_AUX2, sum_bytes)) return -1;
-    Fp2* part = chunks > 1 ? ws<Fp2>(c, WS_PARTIALS) : out;
-    uint64_t* sums = ws<uint64_t>(c, WS_AUX2);
+    p->part_bytes = p->chunks > 1 ? bytes : 0;
+    return 0;
+}
+
+// Every partial and every coefficient sum the kernels read is written earlier
+// in the same call (each (chunk, combination, column) exactly once), so the
+// buffers need no clearing.
+static int combine_launch(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
+                          size_t cols, size_t pad, size_t combinations, Fp2* out, const CombinePlan& pl, Fp2* part,
+                          uint64_t* sums) {
+    const size_t chunk = pl.chunk, chunks = pl.chunks, msg_len = pl.msg_len;
+    if (chunks == 1) part = out;  // one chunk: the partials are the result
     hipLaunchKernelGGL(coeff_chunk_sums, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(combinations)),
                        dim3(256), 0, c->stream, coeffs, sums, rows, chunk);
     VMX_HIP(c, hipGetLastError());
-    const dim3 grid(static_cast<unsigned>(col_blocks), static_cast<unsigned>(chunks));
+    const dim3 grid(static_cast<unsigned>(pl.col_blocks), static_cast<unsigned>(chunks));
     // Vector row loads need a base and a row pitch aligned to CI_COLS i16.
     const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * CI_COLS) == 0) && (cols % CI_COLS == 0);
     if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
@@ -365,16 +382,73 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
     if (pad) {
         const dim3 g(static_cast<unsigned>((pad + 255) / 256), static_cast<unsigned>(chunks),
                      static_cast<unsigned>(combinations));
-        if (combinations > 65535) return fail_msg(c, "too many PCS combinations");
         hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs, part, rows, cols, pad,
                            msg_len, combinations, chunk);
         VMX_HIP(c, hipGetLastError());
     }
     if (chunks == 1) return 0;
-    hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
-                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
+    hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((pl.per_chunk + RED_Z - 1) / RED_Z)),
+                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks,
+                       pl.per_chunk);
     VMX_HIP(c, hipGetLastError());
     return 0;
+}
+
+int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
+                     size_t cols, size_t pad, size_t combinations, Fp2* out) {
+    CombinePlan pl{};
+    if (combine_plan(c, rows, cols, pad, combinations, &pl)) return -1;
+    if ((pl.part_bytes && ensure_ws(c, WS_PARTIALS, pl.part_bytes)) || ensure_ws(c, WS_AUX2, pl.sum_bytes)) return -1;
+    return combine_launch(c, w, pads, coeffs, rows, cols, pad, combinations, out, pl,
+                          pl.part_bytes ? ws<Fp2>(c, WS_PARTIALS) : nullptr, ws<uint64_t>(c, WS_AUX2));
+}
+
+// ---- the allocation-free combination ------------------------------------------------
+// A file-scope scratch array serves the partials and coefficient sums of
+// pcs_combine_rows_noalloc, so that entry point allocates nothing.  Host code
+// never uses the array's name as an address: combine_scratch_attach resolves
+// this device's copy once (hipGetSymbolAddress, with the device current) and
+// every launch takes that pointer.  All calls on one GPU share its array.
+static __device__ __align__(256) unsigned char combine_scratch[COMBINE_SCRATCH_BYTES];
+
+int combine_scratch_attach(Context* c) {
+    static std::mutex mu;
+    static std::map<int, void*> by_device;  // each device's address of combine_scratch
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = by_device.find(c->device);
+    if (it == by_device.end()) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(combine_scratch));
+        if (e != hipSuccess || !p) {
+            c->scratch = nullptr;
+            c->scratch_error = std::string("hipGetSymbolAddress(combine_scratch) failed: ") +
+                               (e != hipSuccess ? hipGetErrorString(e) : "null address");
+            return -1;
+        }
+        it = by_device.emplace(c->device, p).first;
+    }
+    c->scratch = it->second;
+    return 0;
+}
+
+int pcs_combine_rows_noalloc(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
+                             size_t cols, size_t pad, size_t combinations, Fp2* out) {
+    CombinePlan pl{};
+    if (combine_plan(c, rows, cols, pad, combinations, &pl)) return -1;
+    if (!c->scratch) {
+        std::string m = "allocation-free PCS combination unavailable on this device: " + c->scratch_error;
+        return fail_msg(c, m.c_str());
+    }
+    const size_t part_span = (pl.part_bytes + 255) / 256 * 256;
+    if (part_span + pl.sum_bytes > COMBINE_SCRATCH_BYTES) {
+        std::string m = "allocation-free PCS combination needs " + std::to_string(part_span + pl.sum_bytes) +
+                        " bytes of scratch; its fixed array holds " + std::to_string(COMBINE_SCRATCH_BYTES);
+        return fail_msg(c, m.c_str());
+    }
+    unsigned char* base = static_cast<unsigned char*>(c->scratch);
+    return combine_launch(c, w, pads, coeffs, rows, cols, pad, combinations, out, pl,
+                          pl.part_bytes ? reinterpret_cast<Fp2*>(base) : nullptr,
+                          reinterpret_cast<uint64_t*>(base + part_span));
 }
 
 int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, const Fp2* coeffs,

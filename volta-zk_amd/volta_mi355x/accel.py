@@ -150,6 +150,8 @@ _SIGS = {
     "volta_mi355x_ntt_fp_encode_device": (_int, [_vp, _u64, _sz, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_pcs_encode_device": (_int, [_vp, _u64, _sz, _u64, _sz, _sz, _sz, _sz, _sz, _u64, _sz]),
     "volta_mi355x_combine_rows_fp_device": (_int, [_vp, _u64, _sz, _sz, _sz, _u64, _sz, _sz, _u64, _sz]),
+    "volta_mi355x_pcs_combine_rows_device_noalloc": (_int, [_vp, _u64, _sz, _u64, _sz, _u64, _sz, _sz, _sz, _sz, _sz,
+                                                            _u64, _sz]),
     "volta_mi355x_resident_device_ptr": (_int, [_vp, _u64, _sz, _sz, ctypes.POINTER(_vp)]),
     "volta_mi355x_stream": (_int, [_vp, ctypes.POINTER(_vp)]),
     "volta_mi355x_synchronize": (_int, [_vp]),
