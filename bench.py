@@ -5,9 +5,12 @@
 
 One step = one pass of the hot path over the resident synthetic batch of the
 chosen configuration (default C3, the full GPT-2-small weight commit):
-RS-encode of every row (fused i16 lift + NTT) plus the two challenge-power
-row combinations (Fp2 powers + one combination pass).  Inputs are resident
-in HBM before timing starts; outputs stay resident.
+RS-encode of every row through the reference's own calls
+(volta_cuda_pcs_messages_device then volta_cuda_ntt_fp_batch_device, as
+finish_resident_commit makes them; the library encodes straight from the i16
+weights) plus the two challenge-power row combinations (Fp2 powers + one
+combination pass).  Inputs are resident in HBM before timing starts; outputs
+stay resident.
 
 Prints one JSON line: whole-step throughput in codeword Gelem/s, the
 roofline of the dominant kernel (the encode) from HIP events recorded by the
@@ -76,6 +79,7 @@ class Workload:
             self.host_w = w
             self.w = keep(b.upload_device(w.reshape(-1)))
             self.pads = keep(b.alloc_device(1, np.uint64))
+            self.msgs = keep(b.alloc_device(rows * n, np.uint64))
             self.enc = keep(b.alloc_device(rows * n, np.uint64))
             self.challenges = W.challenges_fp2(f"volta-mi355x/{name}/challenges", cfg.combinations)
             self.coeffs = keep(b.alloc_device(cfg.combinations * rows, FP2))
@@ -99,6 +103,7 @@ class Workload:
             self.w = keep(b.upload_device(w))
             del w
             self.pads = keep(b.alloc_device(rows * cfg.pad, np.uint64))
+            self.msgs = keep(b.alloc_device(rows * n, np.uint64))
             self.enc = keep(b.alloc_device(rows * n, np.uint64))
             self.seed = (__import__("ctypes").c_uint8 * 32).from_buffer_copy(W.seed_bytes(f"volta-mi355x/{name}/pads"))
         elif name == "c5":
@@ -124,8 +129,11 @@ class Workload:
         L, r, cfg = self.lib, self.raw, self.cfg
         rows, n = cfg.rows, cfg.n
         if self.name in ("c2", "c3"):
-            self._ok(L.volta_mi355x_pcs_encode_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, 0, n,
-                                                      self.enc.id, 0))
+            # the reference's commit calls (ligero.rs:477-496): message rows,
+            # then the batched NTT of those rows, which encodes from the weights
+            self._ok(L.volta_cuda_pcs_messages_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, 0, n,
+                                                      self.msgs.id, 0))
+            self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
             for k, c in enumerate(self.challenges):
                 self._ok(L.volta_cuda_fp2_powers_device(r, int(c[0]), int(c[1]), self.coeffs.id, k * rows, rows))
             self._ok(L.volta_cuda_pcs_combine_rows_device(r, self.w.id, 0, self.pads.id, 0, self.coeffs.id, 0, rows,
@@ -137,11 +145,13 @@ class Workload:
         elif self.name == "c4":
             self._ok(L.volta_mi355x_ntt_fp_encode_device(r, self.msgs.id, 0, rows, cfg.msg_len, n, self.enc.id, 0))
         elif self.name in ("p15", "p17"):
-            # the resident commit's pads, then lift(w) || pads || 0 encoded in one launch
+            # the resident commit's calls (ligero.rs:474-496): pads, message rows
+            # lift(w) || pads || 0, then their NTT (encoded from the sources)
             self._ok(L.volta_cuda_chacha8_prover_secret_fp_rows_device(r, self.pads.id, 0, self.seed, 0, rows,
                                                                        cfg.pad))
-            self._ok(L.volta_mi355x_pcs_encode_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, cfg.pad, n,
-                                                      self.enc.id, 0))
+            self._ok(L.volta_cuda_pcs_messages_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, cfg.pad,
+                                                      n, self.msgs.id, 0))
+            self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
         elif self.name == "c5":
             self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
             self._ok(L.volta_mi355x_ntt_fp_inverse_batch_device(r, self.enc.id, 0, rows, n, self.back.id, 0))
@@ -179,6 +189,72 @@ def copy_bandwidth(b, nbytes: int = 1 << 32, reps: int = 10) -> float:
     b.free_device(src)
     b.free_device(dst)
     return 2 * nbytes / dt / 1e9
+
+
+def expand_bandwidth(b, src_bytes: int = 1 << 28, reps: int = 20) -> float:
+    """Achievable HBM bandwidth for the encode's traffic shape: src_bytes read,
+    16 x src_bytes written with the encode's 8-byte non-temporal stores
+    (C3's 256 MiB of i16 in, 4 GiB of codewords out)."""
+    import numpy as np
+    src = b.alloc_device(src_bytes // 8, np.uint64)
+    dst = b.alloc_device(src_bytes * 2, np.uint64)
+    b.zero_device(src, 0, src_bytes // 8)
+    L, r = b.lib, b.raw
+    b._check(L.volta_mi355x_probe_expand_device(r, src.id, dst.id, src_bytes))
+    b.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        b._check(L.volta_mi355x_probe_expand_device(r, src.id, dst.id, src_bytes))
+    b.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    b.free_device(src)
+    b.free_device(dst)
+    return 17 * src_bytes / dt / 1e9
+
+
+def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
+    """The reference's unchanged commit calls (finish_resident_commit,
+    ligero.rs:477-496): volta_cuda_pcs_messages_device then
+    volta_cuda_ntt_fp_batch_device on the message rows, timed per chain with
+    the library's HIP events after the timed steps (not part of `value`).
+    `fused`: the calls as Rust makes them (the rows stay unwritten and the
+    transform encodes from the weights); `written`: the same calls with the
+    rows forced into HBM before the transform (a device-pointer query reads
+    the buffer), i.e. the chain without the deferral."""
+    import numpy as np
+    if wl.name not in ("c2", "c3"):
+        return None
+    cfg = wl.cfg
+    rows, n = cfg.rows, cfg.n
+    msgs = wl.msgs
+    L, r = b.lib, b.raw
+
+    def chain(force):
+        wl._ok(L.volta_cuda_pcs_messages_device(r, wl.w.id, 0, wl.pads.id, 0, rows, cfg.msg_len, 0, n, msgs.id, 0))
+        if force:
+            b.device_ptr(msgs)
+        wl._ok(L.volta_cuda_ntt_fp_batch_device(r, msgs.id, 0, rows, n, wl.enc.id, 0))
+
+    out = {"calls": "volta_cuda_pcs_messages_device + volta_cuda_ntt_fp_batch_device", "rows": rows,
+           "code_len": n, "algorithmic_bytes": cfg.algorithmic_bytes, "reps": reps}
+    for force in (False, True):
+        for _ in range(2):
+            chain(force)
+        b.synchronize()
+        b.reset_stats()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            chain(force)
+        b.synchronize()
+        wall = (time.perf_counter() - t0) / reps
+        s = b.get_stats()
+        ntt_ms = s["kernel_ns"]["pcs_ntt"] / reps / 1e6
+        key = "written" if force else "fused"
+        out[key] = {"ms_per_chain": round(wall * 1e3, 4), "ntt_call_ms": round(ntt_ms, 4),
+                    "messages_call_ms": round(s["kernel_ns"]["pcs_rows"] / reps / 1e6, 4),
+                    "achieved_gbs": round(cfg.algorithmic_bytes / wall / 1e9, 1),
+                    "frac_of_peak": round(cfg.algorithmic_bytes / wall / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def fp2_chain_peak(b, log_n: int = 20, rounds: int = 256, reps: int = 10) -> dict:
@@ -321,10 +397,21 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
         "value": round(sample * cfg.n / t / 1e9, 4),
         "unit": "Gelem/s",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{sample} of {cfg.rows} rows of {name} (encode + {cfg.combinations} combinations over those rows), "
                   f"median of 3 after 1 warmup, {t:.3f} s",
     }
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def traffic_for(name: str):
@@ -348,6 +435,7 @@ def main() -> int:
     ap.add_argument("--no-copy-probe", action="store_true")
     ap.add_argument("--no-commit-tree", action="store_true")
     ap.add_argument("--no-x4", action="store_true")
+    ap.add_argument("--no-seam-chain", action="store_true")
     ap.add_argument("--x4-log-n", type=int, default=24)
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -387,7 +475,12 @@ def main() -> int:
     if not a.no_x4:
         log(f"X4 transforms at 2^{a.x4_log_n} points")
         x4 = x4_transforms(b, a.x4_log_n)
+    chain_leg = None
+    if not a.no_seam_chain:
+        log("seam chain (messages + NTT through the reference's calls)")
+        chain_leg = seam_chain(b, wl)
     copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
+    expand_gbs = None if a.no_copy_probe else round(expand_bandwidth(b), 1)
     chain = None if a.no_copy_probe else fp2_chain_peak(b)
     wl_close = wl.close
     cpu = None
@@ -423,10 +516,13 @@ def main() -> int:
             "avg_launch_ms": round(enc_s * 1e3, 4),
             "launches_per_step": launches_per_step,
             "hbm_copy_gbs": copy_gbs,
+            "hbm_expand_gbs": expand_gbs,
+            "frac_of_expand": round(achieved / expand_gbs, 4) if achieved and expand_gbs else None,
         },
         "int_peak": chain,
         "cpu_baseline": cpu,
         "kernel_ms_per_step": {k: round(v / a.steps / 1e6, 4) for k, v in stats["kernel_ns"].items() if v},
+        "seam_chain": chain_leg,
         "commit_tree": tree,
         "x4": x4,
     }

@@ -399,6 +399,10 @@ int volta_mi355x_synchronize(void* ctx);
  * and the reference's Fp2-multiply stream (rounds == 0) / chain kernels
  * (cuda/p7_goldilocks_roofline.cu:74-89).  Not timed or accounted in stats. */
 int volta_mi355x_probe_copy_device(void* ctx, uint64_t src_id, uint64_t dst_id, size_t bytes);
+/* The encode's traffic shape: src_bytes read (a multiple of 256), 16 x
+ * src_bytes written with 8-byte non-temporal stores, 512 contiguous bytes per
+ * wave instruction; dst holds 16 x src_bytes. */
+int volta_mi355x_probe_expand_device(void* ctx, uint64_t src_id, uint64_t dst_id, size_t src_bytes);
 int volta_mi355x_probe_fp2_device(void* ctx, uint64_t a_id, uint64_t b_id, uint64_t out_id, size_t n, int rounds);
 
 #ifdef __cplusplus

@@ -62,8 +62,27 @@ int resident_ntt(Context* c, const uint64_t* in, size_t in_stride, size_t msg_le
 // Resident NTTs
 // ---------------------------------------------------------------------------
 
+// The fused encode of deferred message rows: codewords NTT(lift(w) || pads || 0)
+// read from the i16 weights and the pads, the same result as the transform of
+// the written rows.  `pm` stays pending: its rows are still unwritten.
+static int encode_pending(Context* c, const PendingMessages& pm, uint64_t* out) {
+    uint64_t h2d = 0;
+    TwiddleSet* t = nullptr;
+    if (ensure_twiddles(c, pm.code_len, &h2d, &t)) return -1;
+    if (begin_op(c) || mark_op(c, 1)) return -1;
+    int rc = 1;
+    if (pm.pad == 0) rc = encode_i16_fast(c, pm.w, pm.rows, pm.cols, pm.code_len, out, t);
+    if (rc < 0) return -1;
+    if (rc == 1 && ntt_msg_i16_rows(c, pm.w, pm.pads, pm.rows, pm.cols, pm.pad, pm.code_len, out, t)) return -1;
+    if (mark_op(c, 2)) return -1;
+    return finish_op(c, OP_PCS_NTT, h2d, 0);
+}
+
 // Replaces volta_cuda_ntt_fp_batch_device (cuda/volta_cuda_backend.cu:6545-6561):
 // out-of-place batched forward NTT of pre-padded rows; input is preserved.
+// When the input is exactly the region of deferred message rows (the
+// reference's commit chain), the codewords are encoded from their sources in
+// one pass; the rows stay deferred.
 VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_off, size_t rows, size_t n,
                                               uint64_t out_id, size_t out_off) {
     Context* c = static_cast<Context*>(raw);
@@ -71,8 +90,21 @@ VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_
     return guarded(c, "resident Fp NTT", [&] {
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp NTT geometry overflows size_t");
+        const PendingMessages& pm = c->pending;
+        if (c->has_pending && pm.out_id == in_id && pm.out_off == in_off && pm.rows == rows && pm.code_len == n &&
+            out_id != pm.w_id && (!pm.pad || out_id != pm.pads_id)) {
+            c->bypass_settle = true;
+            void *in = nullptr, *out = nullptr;
+            const int rc = region_elems(c, in_id, in_off, total, 8, &in) ||
+                           region_elems(c, out_id, out_off, total, 8, &out);
+            c->bypass_settle = false;
+            if (rc) return -1;
+            if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
+                return fail_msg(c, "resident Fp NTT input and output overlap");
+            return encode_pending(c, pm, static_cast<uint64_t*>(out));
+        }
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
+        if (region_elems(c, in_id, in_off, total, 8, &in, true) || region_elems(c, out_id, out_off, total, 8, &out))
             return -1;
         if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident Fp NTT input and output overlap");
@@ -91,7 +123,7 @@ VMX_API int volta_cuda_ntt_fp2_batch_device(void* raw, uint64_t in_id, size_t in
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident Fp2 NTT geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, total, 16, &in) || region_elems(c, out_id, out_off, total, 16, &out))
+        if (region_elems(c, in_id, in_off, total, 16, &in, true) || region_elems(c, out_id, out_off, total, 16, &out))
             return -1;
         if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident Fp2 NTT input and output overlap");
@@ -185,13 +217,31 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
         if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(rows, code_len, &on))
             return fail_msg(c, "resident PCS message geometry overflows size_t");
         void *w = nullptr, *pads = nullptr, *out = nullptr;
-        if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
-            region_elems(c, out_id, out_off, on, 8, &out))
+        if (region_elems(c, w_id, w_off, wn, 2, &w, true) ||
+            (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads, true)))
             return -1;
+        // Deferred rows of exactly this region are replaced by this call's.
+        if (c->has_pending && c->pending.out_id == out_id && c->pending.out_off == out_off &&
+            c->pending.rows * c->pending.code_len == on)
+            c->has_pending = false;
+        if (region_elems(c, out_id, out_off, on, 8, &out)) return -1;
         if (begin_op(c) || mark_op(c, 1)) return -1;
-        if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols, pad,
-                         code_len, static_cast<uint64_t*>(out)))
+        // The rows are recorded, not written, when their buffer is separate
+        // from the sources: a following forward NTT of exactly these rows
+        // (finish_resident_commit, rust/volta-pcs/src/ligero.rs:477-496) then
+        // encodes straight from the weights and pads, and any other access
+        // writes them first (settle_pending).  The stats are those of a
+        // messages call either way.
+        if (out_id != w_id && (!pad || out_id != pads_id)) {
+            if (c->has_pending && settle_pending(c)) return -1;  // one record at a time
+            c->pending = PendingMessages{out_id, out_off, static_cast<uint64_t*>(out), w_id, pad ? pads_id : 0,
+                                         static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
+                                         rows, cols, pad, code_len};
+            c->has_pending = true;
+        } else if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols,
+                                pad, code_len, static_cast<uint64_t*>(out))) {
             return -1;
+        }
         if (mark_op(c, 2)) return -1;
         return finish_op(c, OP_PCS_ROWS, 0, 0);
     });
@@ -206,8 +256,8 @@ int combine_device(Context* c, uint64_t w_id, size_t w_off, uint64_t pads_id, si
         !add_ok(cols, pad, &msg_len) || !mul_ok(combinations, msg_len, &on))
         return fail_msg(c, "resident PCS combination geometry overflows size_t");
     void *w = nullptr, *pads = nullptr, *co = nullptr, *out = nullptr;
-    if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
-        region_elems(c, co_id, co_off, cn, 16, &co) || region_elems(c, out_id, out_off, on, 16, &out))
+    if (region_elems(c, w_id, w_off, wn, 2, &w, true) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads, true)) ||
+        region_elems(c, co_id, co_off, cn, 16, &co, true) || region_elems(c, out_id, out_off, on, 16, &out))
         return -1;
     if (begin_op(c) || mark_op(c, 1)) return -1;
     const auto combine = noalloc ? pcs_combine_rows_noalloc : pcs_combine_rows;
@@ -301,7 +351,7 @@ VMX_API int volta_cuda_fp2_add_inplace_device(void* raw, uint64_t t_id, size_t t
     if (!c || !n) return fail_msg(c, "invalid resident Fp2 add");
     return guarded(c, "resident Fp2 add", [&] {
         void *t = nullptr, *a = nullptr;
-        if (region_elems(c, t_id, t_off, n, 16, &t) || region_elems(c, a_id, a_off, n, 16, &a)) return -1;
+        if (region_elems(c, t_id, t_off, n, 16, &t) || region_elems(c, a_id, a_off, n, 16, &a, true)) return -1;
         if (begin_op(c) || mark_op(c, 1)) return -1;
         if (fp2_add_inplace(c, static_cast<Fp2*>(t), static_cast<const Fp2*>(a), n)) return -1;
         if (mark_op(c, 2)) return -1;
@@ -321,7 +371,7 @@ VMX_API int volta_cuda_pcs_gather_columns_device(void* raw, uint64_t m_id, size_
         if (!mul_ok(rows, cols, &mn) || !mul_ok(rows, queries, &on))
             return fail_msg(c, "resident PCS gather geometry overflows size_t");
         void *m = nullptr, *idx = nullptr, *out = nullptr;
-        if (region_elems(c, m_id, m_off, mn, elem, &m) || region_elems(c, idx_id, idx_off, queries, 4, &idx) ||
+        if (region_elems(c, m_id, m_off, mn, elem, &m, true) || region_elems(c, idx_id, idx_off, queries, 4, &idx, true) ||
             region_elems(c, out_id, out_off, on, elem, &out))
             return -1;
         // Indices live on the device and are validated by the Rust seam before
@@ -443,7 +493,7 @@ VMX_API int volta_mi355x_ntt_fp_inverse_batch_device(void* raw, uint64_t in_id, 
         size_t total = 0;
         if (!mul_ok(rows, n, &total)) return fail_msg(c, "resident inverse Fp NTT geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, total, 8, &in) || region_elems(c, out_id, out_off, total, 8, &out))
+        if (region_elems(c, in_id, in_off, total, 8, &in, true) || region_elems(c, out_id, out_off, total, 8, &out))
             return -1;
         if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident inverse Fp NTT input and output overlap");
@@ -463,7 +513,7 @@ VMX_API int volta_mi355x_ntt_fp_encode_device(void* raw, uint64_t in_id, size_t 
         if (!mul_ok(rows, msg_len, &in_n) || !mul_ok(rows, n, &out_n))
             return fail_msg(c, "resident Fp encode geometry overflows size_t");
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, std::max<size_t>(in_n, 1), 8, &in) ||
+        if (region_elems(c, in_id, in_off, std::max<size_t>(in_n, 1), 8, &in, true) ||
             region_elems(c, out_id, out_off, out_n, 8, &out))
             return -1;
         if (in_id == out_id) return fail_msg(c, "resident Fp encode input and output must be distinct buffers");
@@ -487,7 +537,7 @@ VMX_API int volta_mi355x_pcs_encode_device(void* raw, uint64_t w_id, size_t w_of
         if (!mul_ok(rows, cols, &wn) || !mul_ok(rows, pad, &pn) || !mul_ok(rows, code_len, &on))
             return fail_msg(c, "resident PCS encode geometry overflows size_t");
         void *w = nullptr, *pads = nullptr, *out = nullptr;
-        if (region_elems(c, w_id, w_off, wn, 2, &w) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads)) ||
+        if (region_elems(c, w_id, w_off, wn, 2, &w, true) || (pad && region_elems(c, pads_id, pads_off, pn, 8, &pads, true)) ||
             region_elems(c, out_id, out_off, on, 8, &out))
             return -1;
         uint64_t h2d = 0;
@@ -521,7 +571,7 @@ VMX_API int volta_mi355x_combine_rows_fp_device(void* raw, uint64_t m_id, size_t
         if (!mul_ok(rows, cols, &mn) || !mul_ok(combinations, rows, &cn) || !mul_ok(combinations, cols, &on))
             return fail_msg(c, "resident Fp combination geometry overflows size_t");
         void *m = nullptr, *co = nullptr, *out = nullptr;
-        if (region_elems(c, m_id, m_off, mn, 8, &m) || region_elems(c, co_id, co_off, cn, 16, &co) ||
+        if (region_elems(c, m_id, m_off, mn, 8, &m, true) || region_elems(c, co_id, co_off, cn, 16, &co, true) ||
             region_elems(c, out_id, out_off, on, 16, &out))
             return -1;
         if (begin_op(c) || mark_op(c, 1)) return -1;
@@ -555,8 +605,18 @@ VMX_API int volta_mi355x_probe_copy_device(void* raw, uint64_t src_id, uint64_t 
     Context* c = static_cast<Context*>(raw);
     if (!c || !bytes || bytes % 16) return fail_msg(c, "invalid copy probe geometry (bytes must be a multiple of 16)");
     void *s = nullptr, *d = nullptr;
-    if (region(c, src_id, 0, bytes, &s) || region(c, dst_id, 0, bytes, &d)) return -1;
+    if (region(c, src_id, 0, bytes, &s, true) || region(c, dst_id, 0, bytes, &d)) return -1;
     return probe_copy(c, s, d, bytes);
+}
+
+VMX_API int volta_mi355x_probe_expand_device(void* raw, uint64_t src_id, uint64_t dst_id, size_t src_bytes) {
+    Context* c = static_cast<Context*>(raw);
+    if (!c || !src_bytes || src_bytes % 256) return fail_msg(c, "invalid expand probe geometry (a multiple of 256 bytes)");
+    size_t dst_bytes = 0;
+    if (!mul_ok(src_bytes, 16, &dst_bytes)) return fail_msg(c, "expand probe geometry overflows size_t");
+    void *s = nullptr, *d = nullptr;
+    if (region(c, src_id, 0, src_bytes, &s, true) || region(c, dst_id, 0, dst_bytes, &d)) return -1;
+    return probe_expand(c, s, d, src_bytes);
 }
 
 VMX_API int volta_mi355x_probe_fp2_device(void* raw, uint64_t a_id, uint64_t b_id, uint64_t out_id, size_t n,
@@ -564,7 +624,7 @@ VMX_API int volta_mi355x_probe_fp2_device(void* raw, uint64_t a_id, uint64_t b_i
     Context* c = static_cast<Context*>(raw);
     if (!c || !n || rounds < 0) return fail_msg(c, "invalid Fp2 probe geometry");
     void *a = nullptr, *b = nullptr, *o = nullptr;
-    if (region_elems(c, a_id, 0, n, 16, &a) || region_elems(c, b_id, 0, n, 16, &b) ||
+    if (region_elems(c, a_id, 0, n, 16, &a, true) || region_elems(c, b_id, 0, n, 16, &b, true) ||
         region_elems(c, out_id, 0, n, 16, &o))
         return -1;
     if (rounds == 0)
@@ -601,7 +661,7 @@ int hash_tree_device(Context* c, uint64_t m_id, size_t m_off, size_t rows, size_
     if (!mul_ok(rows, cols, &mn) || !mul_ok(2 * cols - 1, 32, &tb))
         return fail_msg(c, "resident Merkle geometry overflows size_t");
     void *m = nullptr, *tree = nullptr;
-    if (region_elems(c, m_id, m_off, mn, fp2 ? 16 : 8, &m) || region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree))
+    if (region_elems(c, m_id, m_off, mn, fp2 ? 16 : 8, &m, true) || region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree))
         return -1;
     if (hash_aligned(c, tree, "Merkle tree")) return -1;
     if (begin_op(c) || mark_op(c, 1)) return -1;
@@ -653,8 +713,8 @@ VMX_API int volta_cuda_merkle_paths_device(void* raw, uint64_t tree_id, size_t t
         if (!mul_ok(2 * leaves - 1, 32, &tb) || !mul_ok(queries * bits, 32, &pb))
             return fail_msg(c, "resident Merkle path geometry overflows size_t");
         void *tree = nullptr, *idx = nullptr, *paths = nullptr;
-        if (region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree) ||
-            region_elems(c, idx_id, idx_off, queries, 4, &idx) ||
+        if (region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree, true) ||
+            region_elems(c, idx_id, idx_off, queries, 4, &idx, true) ||
             region_elems(c, paths_id, paths_off_bytes, pb, 1, &paths))
             return -1;
         if (hash_aligned(c, tree, "Merkle tree") || hash_aligned(c, paths, "Merkle path")) return -1;
@@ -710,7 +770,7 @@ VMX_API int volta_cuda_logup_eq_rows_device(void* raw, uint64_t points_id, size_
         if (!mul_ok(rows, width, &total) || !mul_ok(rows, dims, &pn))
             return fail_msg(c, "resident eq-row geometry overflows size_t");
         void *points = nullptr, *out = nullptr;
-        if ((dims && region_elems(c, points_id, points_off, pn, 16, &points)) ||
+        if ((dims && region_elems(c, points_id, points_off, pn, 16, &points, true)) ||
             region_elems(c, out_id, out_off, total, 16, &out))
             return -1;
         if (begin_op(c) || mark_op(c, 1)) return -1;
@@ -736,8 +796,8 @@ VMX_API int volta_cuda_fp2_row_dots_device(void* raw, uint64_t a_id, size_t a_of
             return fail_msg(c, "Fp2 row-dot geometry overflows size_t");
         void *a = nullptr, *b = nullptr, *out = nullptr;
         size_t a_span = 0, b_span = 0;
-        if (strided_region(c, a_id, aob, asb, rowb, rows, &a, &a_span) ||
-            strided_region(c, b_id, bob, bsb, rowb, rows, &b, &b_span) ||
+        if (strided_region(c, a_id, aob, asb, rowb, rows, &a, &a_span, true) ||
+            strided_region(c, b_id, bob, bsb, rowb, rows, &b, &b_span, true) ||
             region_elems(c, out_id, out_off, rows, 16, &out))
             return -1;
         auto overlaps = [&](const void* p, size_t n) {
@@ -813,7 +873,7 @@ VMX_API int volta_mi355x_x4_ntt_fp2_device(void* raw, uint64_t in_id, size_t in_
     if (!c || !len || len > n || !pow2(n) || n > X4_MAX_N) return fail_msg(c, "invalid resident X4 NTT geometry");
     return guarded(c, "resident X4 NTT", [&] {
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, len, sizeof(Fp2), &in) ||
+        if (region_elems(c, in_id, in_off, len, sizeof(Fp2), &in, true) ||
             region_elems(c, out_id, out_off, n, sizeof(Fp2), &out))
             return -1;
         const auto a = reinterpret_cast<uintptr_t>(in), b = reinterpret_cast<uintptr_t>(out);

@@ -90,7 +90,25 @@ Resident* find_resident(Context* c, uint64_t id) {
     return (r.active && r.generation == gen) ? &r : nullptr;
 }
 
-int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out) {
+int settle_pending(Context* c) {
+    if (!c->has_pending) return 0;
+    const PendingMessages m = c->pending;
+    c->has_pending = false;
+    return pcs_messages(c, m.w, m.pads, m.rows, m.cols, m.pad, m.code_len, m.out);
+}
+
+// Every entry point reaches resident memory through region(), so deferred
+// message rows are written here before anything can read them or overwrite
+// their sources (freeing a source writes them too, resident_free).
+static bool touches_pending(const Context* c, uint64_t id, bool read_only) {
+    const PendingMessages& m = c->pending;
+    if (id == m.out_id) return true;
+    return !read_only && (id == m.w_id || (m.pad && id == m.pads_id));
+}
+
+int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out, bool read_only) {
+    if (c && c->has_pending && !c->bypass_settle && touches_pending(c, id, read_only) && settle_pending(c))
+        return -1;
     Resident* r = find_resident(c, id);
     if (!r) return fail_msg(c, "unknown resident buffer id");
     if (offset_bytes > r->logical || bytes > r->logical - offset_bytes)
@@ -99,21 +117,21 @@ int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** ou
     return 0;
 }
 
-int region_elems(Context* c, uint64_t id, size_t offset, size_t count, size_t elem, void** out) {
+int region_elems(Context* c, uint64_t id, size_t offset, size_t count, size_t elem, void** out, bool read_only) {
     size_t ob = 0, nb = 0;
     if (!mul_ok(offset, elem, &ob) || !mul_ok(count, elem, &nb))
         return fail_msg(c, "resident region geometry overflows size_t");
-    return region(c, id, ob, nb, out);
+    return region(c, id, ob, nb, out, read_only);
 }
 
 int strided_region(Context* c, uint64_t id, size_t offset, size_t stride, size_t row_bytes,
-                   size_t rows, void** out, size_t* span) {
+                   size_t rows, void** out, size_t* span, bool read_only) {
     if (!rows || !row_bytes || stride < row_bytes)
         return fail_msg(c, "invalid resident strided-row geometry");
     size_t prefix = 0;
     if (!mul_ok(rows - 1, stride, &prefix) || !add_ok(prefix, row_bytes, span))
         return fail_msg(c, "resident strided-row geometry overflows size_t");
-    return region(c, id, offset, *span, out);
+    return region(c, id, offset, *span, out, read_only);
 }
 
 // ---- synchronisation ---------------------------------------------------------
@@ -1049,6 +1067,13 @@ VMX_API int volta_cuda_resident_free(void* raw, uint64_t id) {
     ++c->stats.resident_free_requests;
     Resident* r = find_resident(c, id);
     if (!r) return fail_msg(c, "unknown or stale resident buffer id");
+    // Freeing the buffer that holds deferred message rows discards them;
+    // freeing one of their sources writes them first.
+    if (c->has_pending) {
+        if (c->pending.out_id == id) c->has_pending = false;
+        else if ((c->pending.w_id == id || (c->pending.pad && c->pending.pads_id == id)) && settle_pending(c))
+            return -1;
+    }
     // Storage stays cached for reuse; single-stream ordering makes a later
     // user of the same storage run after every earlier user.
     c->free_slots.push_back(static_cast<size_t>((id & 0xFFFFFFFFull) - 1));
@@ -1077,7 +1102,7 @@ VMX_API int volta_cuda_resident_download(void* raw, uint64_t id, size_t off, voi
     Context* c = static_cast<Context*>(raw);
     if (!c || !dst || !bytes) return fail_msg(c, "invalid resident download");
     void* src = nullptr;
-    if (region(c, id, off, bytes, &src)) return -1;
+    if (region(c, id, off, bytes, &src, true)) return -1;
     if (begin_transfer(c)) return -1;
     const auto t0 = std::chrono::steady_clock::now();
     const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream);
@@ -1140,7 +1165,7 @@ static int copy_rows_impl(Context* c, uint64_t src_id, size_t src_off, size_t sr
     if (!c) return -1;
     void *src = nullptr, *dst = nullptr;
     size_t src_span = 0, dst_span = 0;
-    if (strided_region(c, src_id, src_off, src_stride, row_bytes, rows, &src, &src_span) ||
+    if (strided_region(c, src_id, src_off, src_stride, row_bytes, rows, &src, &src_span, true) ||
         strided_region(c, dst_id, dst_off, dst_stride, row_bytes, rows, &dst, &dst_span))
         return -1;
     if (src_id == dst_id) {

@@ -205,6 +205,21 @@ struct TwiddleSet {
     size_t n = 0;
 };
 
+// Message rows msg = lift(w) || pads || 0 that volta_cuda_pcs_messages_device
+// recorded but has not written yet (the out region holds them virtually).
+// They are written by settle_pending before any other access to any resident
+// buffer, unless the next access is a forward NTT of exactly that region,
+// which encodes straight from the sources instead.
+struct PendingMessages {
+    uint64_t out_id = 0;
+    size_t out_off = 0;  // elements
+    uint64_t* out = nullptr;
+    uint64_t w_id = 0, pads_id = 0;
+    const int16_t* w = nullptr;
+    const uint64_t* pads = nullptr;
+    size_t rows = 0, cols = 0, pad = 0, code_len = 0;
+};
+
 struct Context {
     int device = 0;
     int cu_count = 0;  // compute units of `device` (sizes persistent grids)
@@ -242,6 +257,11 @@ struct Context {
     // array (null when it could not be resolved)
     void* scratch = nullptr;
     std::string scratch_error;
+    // at most one deferred message-row record; `bypass_settle` lets the NTT
+    // that consumes it resolve its regions without writing it
+    bool has_pending = false;
+    PendingMessages pending{};
+    bool bypass_settle = false;
     std::string error;
 };
 
@@ -261,12 +281,15 @@ bool mul_ok(size_t a, size_t b, size_t* out);
 bool add_ok(size_t a, size_t b, size_t* out);
 Resident* find_resident(Context* c, uint64_t id);
 // Resolve a byte region of a resident buffer; fails if out of bounds.
-int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out);
+// `read_only` marks a region the caller only reads: deferred message rows are
+// written first only when their own buffer is read, while any other access
+// to their buffer or to their sources writes them first.
+int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out, bool read_only = false);
 // Element-offset variant: offset and count in units of elem_bytes.
 int region_elems(Context* c, uint64_t id, size_t offset, size_t count, size_t elem_bytes,
-                 void** out);
+                 void** out, bool read_only = false);
 int strided_region(Context* c, uint64_t id, size_t offset, size_t stride, size_t row_bytes,
-                   size_t rows, void** out, size_t* span);
+                   size_t rows, void** out, size_t* span, bool read_only = false);
 
 // Pinned host regions (byte offsets) and their transfer state: a pinned
 // source stays "in flight" from the copy that reads it until its ready event
@@ -274,6 +297,10 @@ int strided_region(Context* c, uint64_t id, size_t offset, size_t stride, size_t
 int pinned_region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** out, Pinned** owner);
 int pinned_ready(Context* c, Pinned* p, bool* ready);
 int pinned_mark_in_flight(Context* c, Pinned* p);
+
+// Writes the deferred message rows, if any (one launch on the context stream,
+// outside any primitive's timing record).
+int settle_pending(Context* c);
 
 // ---- workspaces and twiddles ---------------------------------------------------
 int ensure_ws(Context* c, int slot, size_t bytes);

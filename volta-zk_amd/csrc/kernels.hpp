@@ -109,6 +109,7 @@ int fp2_mobius(Context* c, gl::Fp2* values, uint64_t n, bool inverse);
 
 // Measurement probes.
 int probe_copy(Context* c, const void* src, void* dst, size_t bytes);
+int probe_expand(Context* c, const void* src, void* dst, size_t src_bytes);
 int probe_fp2_stream(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n);
 int probe_fp2_chain(Context* c, const gl::Fp2* a, const gl::Fp2* b, gl::Fp2* out, size_t n, int rounds);
 

@@ -669,6 +669,28 @@ __global__ __launch_bounds__(256) void copy_kernel(const uint4* src, uint4* dst,
         dst[i] = src[i];
 }
 
+// The encode's traffic shape as a yardstick: every 4 bytes read become 64
+// bytes written (1:16, as i16 messages at rate 1/4 become u64 codewords), with
+// the encode's stores: 8 bytes per lane, 512 contiguous bytes per wave
+// instruction, non-temporal.
+__global__ __launch_bounds__(256) void expand_kernel(const uint32_t* src, uint64_t* dst, size_t n32) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n32; i += stride) {
+        const uint64_t v = src[i];
+        uint64_t* o = dst + (i / 64) * 512 + (i % 64);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) __builtin_nontemporal_store(v + k, o + 64 * k);
+    }
+}
+
+int probe_expand(Context* c, const void* src, void* dst, size_t src_bytes) {
+    const size_t n32 = src_bytes / 4;
+    hipLaunchKernelGGL(expand_kernel, dim3(grid_for(n32, 256 * 4, 256 * 64)), dim3(256), 0, c->stream,
+                       static_cast<const uint32_t*>(src), static_cast<uint64_t*>(dst), n32);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
+
 int probe_copy(Context* c, const void* src, void* dst, size_t bytes) {
     const size_t n16 = bytes / 16;
     hipLaunchKernelGGL(copy_kernel, dim3(grid_for(n16, 256 * 8, 256 * 64)), dim3(256), 0, c->stream,

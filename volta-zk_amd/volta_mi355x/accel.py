@@ -156,6 +156,7 @@ _SIGS = {
     "volta_mi355x_stream": (_int, [_vp, ctypes.POINTER(_vp)]),
     "volta_mi355x_synchronize": (_int, [_vp]),
     "volta_mi355x_probe_copy_device": (_int, [_vp, _u64, _u64, _sz]),
+    "volta_mi355x_probe_expand_device": (_int, [_vp, _u64, _u64, _sz]),
     "volta_mi355x_probe_fp2_device": (_int, [_vp, _u64, _u64, _u64, _sz, _int]),
 }
 
