@@ -79,7 +79,6 @@ class Workload:
             self.host_w = w
             self.w = keep(b.upload_device(w.reshape(-1)))
             self.pads = keep(b.alloc_device(1, np.uint64))
-            self.msgs = keep(b.alloc_device(rows * n, np.uint64))
             self.enc = keep(b.alloc_device(rows * n, np.uint64))
             self.challenges = W.challenges_fp2(f"volta-mi355x/{name}/challenges", cfg.combinations)
             self.coeffs = keep(b.alloc_device(cfg.combinations * rows, FP2))
@@ -103,7 +102,6 @@ class Workload:
             self.w = keep(b.upload_device(w))
             del w
             self.pads = keep(b.alloc_device(rows * cfg.pad, np.uint64))
-            self.msgs = keep(b.alloc_device(rows * n, np.uint64))
             self.enc = keep(b.alloc_device(rows * n, np.uint64))
             self.seed = (__import__("ctypes").c_uint8 * 32).from_buffer_copy(W.seed_bytes(f"volta-mi355x/{name}/pads"))
         elif name == "c5":
@@ -125,15 +123,24 @@ class Workload:
         if rc != 0:
             raise RuntimeError(self.b.last_error())
 
+    def messages_buffer(self, nbytes: int) -> int:
+        """A new resident buffer as Backend::pcs_messages_device allocates one
+        per call (after the first step it reuses the freed storage)."""
+        out = ctypes.c_uint64()
+        self._ok(self.lib.volta_cuda_resident_alloc(self.raw, nbytes, ctypes.byref(out)))
+        return out.value
+
     def step(self):
         L, r, cfg = self.lib, self.raw, self.cfg
         rows, n = cfg.rows, cfg.n
         if self.name in ("c2", "c3"):
-            # the reference's commit calls (ligero.rs:477-496): message rows,
-            # then the batched NTT of those rows, which encodes from the weights
-            self._ok(L.volta_cuda_pcs_messages_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, 0, n,
-                                                      self.msgs.id, 0))
-            self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
+            # the reference's commit calls (ligero.rs:477-496): message rows
+            # into a new buffer, the batched NTT of those rows (encoded from
+            # the weights), the rows freed
+            m = self.messages_buffer(rows * n * 8)
+            self._ok(L.volta_cuda_pcs_messages_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, 0, n, m, 0))
+            self._ok(L.volta_cuda_ntt_fp_batch_device(r, m, 0, rows, n, self.enc.id, 0))
+            self._ok(L.volta_cuda_resident_free(r, m))
             for k, c in enumerate(self.challenges):
                 self._ok(L.volta_cuda_fp2_powers_device(r, int(c[0]), int(c[1]), self.coeffs.id, k * rows, rows))
             self._ok(L.volta_cuda_pcs_combine_rows_device(r, self.w.id, 0, self.pads.id, 0, self.coeffs.id, 0, rows,
@@ -149,9 +156,11 @@ class Workload:
             # lift(w) || pads || 0, then their NTT (encoded from the sources)
             self._ok(L.volta_cuda_chacha8_prover_secret_fp_rows_device(r, self.pads.id, 0, self.seed, 0, rows,
                                                                        cfg.pad))
+            m = self.messages_buffer(rows * n * 8)
             self._ok(L.volta_cuda_pcs_messages_device(r, self.w.id, 0, self.pads.id, 0, rows, cfg.msg_len, cfg.pad,
-                                                      n, self.msgs.id, 0))
-            self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
+                                                      n, m, 0))
+            self._ok(L.volta_cuda_ntt_fp_batch_device(r, m, 0, rows, n, self.enc.id, 0))
+            self._ok(L.volta_cuda_resident_free(r, m))
         elif self.name == "c5":
             self._ok(L.volta_cuda_ntt_fp_batch_device(r, self.msgs.id, 0, rows, n, self.enc.id, 0))
             self._ok(L.volta_mi355x_ntt_fp_inverse_batch_device(r, self.enc.id, 0, rows, n, self.back.id, 0))
@@ -167,7 +176,7 @@ class Workload:
         return self.cfg.elements * (2 if self.name == "c5" else 1)
 
     def close(self):
-        for x in self.bufs:
+        for x in reversed(self.bufs):
             self.b.free_device(x)
 
 
@@ -217,23 +226,26 @@ def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
     ligero.rs:477-496): volta_cuda_pcs_messages_device then
     volta_cuda_ntt_fp_batch_device on the message rows, timed per chain with
     the library's HIP events after the timed steps (not part of `value`).
-    `fused`: the calls as Rust makes them (the rows stay unwritten and the
-    transform encodes from the weights); `written`: the same calls with the
-    rows forced into HBM before the transform (a device-pointer query reads
-    the buffer), i.e. the chain without the deferral."""
+    `fused`: the calls as Rust makes them, the rows' buffer allocated before
+    and freed after (the rows stay unwritten and the transform encodes from
+    the weights); `written`: the same calls with the rows forced into HBM
+    before the transform (a device-pointer query of their buffer), i.e. the
+    chain without the deferral."""
     import numpy as np
     if wl.name not in ("c2", "c3"):
         return None
     cfg = wl.cfg
     rows, n = cfg.rows, cfg.n
-    msgs = wl.msgs
     L, r = b.lib, b.raw
 
     def chain(force):
-        wl._ok(L.volta_cuda_pcs_messages_device(r, wl.w.id, 0, wl.pads.id, 0, rows, cfg.msg_len, 0, n, msgs.id, 0))
+        m = wl.messages_buffer(rows * n * 8)
+        wl._ok(L.volta_cuda_pcs_messages_device(r, wl.w.id, 0, wl.pads.id, 0, rows, cfg.msg_len, 0, n, m, 0))
         if force:
-            b.device_ptr(msgs)
-        wl._ok(L.volta_cuda_ntt_fp_batch_device(r, msgs.id, 0, rows, n, wl.enc.id, 0))
+            p = ctypes.c_void_p()
+            wl._ok(L.volta_mi355x_resident_device_ptr(r, m, 0, 8, ctypes.byref(p)))
+        wl._ok(L.volta_cuda_ntt_fp_batch_device(r, m, 0, rows, n, wl.enc.id, 0))
+        wl._ok(L.volta_cuda_resident_free(r, m))
 
     out = {"calls": "volta_cuda_pcs_messages_device + volta_cuda_ntt_fp_batch_device", "rows": rows,
            "code_len": n, "algorithmic_bytes": cfg.algorithmic_bytes, "reps": reps}
