@@ -124,6 +124,20 @@ def test_forward_and_inverse_2_25(backend, oracle):
     assert (got == oracle.ntt_forward_batch(host)).all()
 
 
+def test_inverse_round_trip_four_passes(backend):
+    """One 2^26 row: four passes of radix 2^7, 2^7, 2^6, 2^6, so the
+    inverse's gather maps rows through two middle digits."""
+    n = 1 << 26
+    host = rand_fp(26, (1, n))
+    inp = backend.upload_device(host.reshape(-1))
+    fwd = backend.ntt_fp_batch_device(inp, 1, n)
+    inv = backend.ntt_fp_inverse_batch_device(fwd, 1, n)
+    back = backend.download_device(inv).reshape(1, n)
+    for b in (inp, fwd, inv):
+        backend.free_device(b)
+    assert (back == host).all()
+
+
 def test_batch_beyond_one_launch_slice(backend, oracle):
     """65,537 rows of 2^13: the pass engine launches at most 65,535 rows per
     grid; rows on both sides of each slice boundary match the oracle."""

@@ -130,6 +130,8 @@ struct SrcU64 {
     __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t nmask) const {
         return reverse ? (uint64_t{0} - idx) & nmask : idx;
     }
+    // Offset of the gather's rows against its tiles (see gather_reg).
+    __device__ __forceinline__ uint32_t rotation() const { return reverse ? 1u : 0u; }
     __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t plane, int PL) const {
         const uint64_t ci = idx < len ? idx : 0;
         return Raw{x[(row * x_stride + ci) * PL + plane]};
@@ -155,6 +157,7 @@ struct SrcMsgI16 {
     };
     __host__ __device__ uint64_t extent(uint64_t n) const { return cols + pad > n ? n : cols + pad; }
     __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t) const { return idx; }
+    __device__ __forceinline__ uint32_t rotation() const { return 0u; }
     __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t, int) const {
         const uint64_t wi = idx < cols ? idx : 0;
         const uint64_t pi = idx >= cols && idx - cols < pad ? idx - cols : 0;
@@ -172,11 +175,32 @@ constexpr uint64_t prefix_mask(int nz, int la) {
     return m;
 }
 
+// Output row of the gather row whose inputs sit at x[L + (n / R) j]
+// (L < n / R, R = 2^rb): i_1 = the low r1 bits of L, most significant in the
+// row index, then the middle digits of L in reverse order (gather_tile's map).
+__device__ __forceinline__ uint64_t gather_row(uint64_t L, const Digits& d, int mid_bits) {
+    const uint64_t i1 = L & ((uint64_t{1} << d.r1) - 1), m = L >> d.r1;
+    uint64_t rest = 0;
+    int shift = mid_bits, scale = 0;
+    for (int j = 0; j < d.count; ++j) {
+        shift -= d.bits[j];
+        rest += ((m >> scale) & ((uint64_t{1} << d.bits[j]) - 1)) << shift;
+        scale += d.bits[j];
+    }
+    return (i1 << mid_bits) + rest;
+}
+
 // Gather pass of row blockIdx.y of a batch: tile of 2^qb rows, inputs from
 // src, output rows n elements apart.  Step 1 reads only ja < NZ: the host
 // picks NZ so that every input with ja >= NZ lies in the zero tail
 // (ja B + jb >= NZ B puts the index at >= NZ n / A >= the source's extent),
 // and the A-point DFT skips the butterflies that only meet those zeros.
+// A source read at (n - idx) mod n (the inverse transform) has rotation 1:
+// lane t of a tile takes row L = nat0 + t + 1 (mod n / R) instead of
+// nat0 + t, so that its reads n - L - (n / R) j of one (ja, jb) cover the
+// aligned run [n / R - nat0 - 2^qb, n / R - nat0) + (n / R)(R - 1 - j): one
+// 128-byte line per run instead of two (only the wrap to L = 0 in the last
+// tile straddles).  The rows still cover 0 .. n / R - 1 once.
 template <int LA, int LB, int PL, int NZ, class Src>
 __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restrict__ y, int nb, int qb, Digits d,
                                                       const uint64_t* inner) {
@@ -199,7 +223,8 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     int mid_bits;
     gather_tile(nb, RB, qb, d, nat0, row0, mid_bits);
     const int sh = nb - RB;
-    const uint64_t nmask = (uint64_t{1} << nb) - 1;
+    const uint64_t nmask = (uint64_t{1} << nb) - 1, lmask = (uint64_t{1} << sh) - 1;
+    const uint32_t rot = sh > 0 ? src.rotation() : 0u;
     // Step 1 (loads, A-point DFTs) issues at a higher wave priority than step 2
     // (B-point DFTs, stores), so co-resident workgroups interleave their
     // phases (measured: C4 +6%, p15 +3%, X4 2^24 +3%, C5 and p17 within 2%).
@@ -207,17 +232,18 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     for (uint32_t job = threadIdx.x; job < (PW << LB); job += THREADS) {
         const uint32_t pc = job & (PW - 1), jb = job >> pwb;
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
+        const uint64_t L = (nat0 + t + rot) & lmask;
         typename Src::Raw raw[NZ];
         gl::static_for<0, NZ>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
-            const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
+            const uint64_t idx = src.index(L + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
             raw[ja] = src.fetch(row, idx, plane, PL);
         });
         uint64_t v[A];
         gl::static_for<0, A>([&](auto i_) { v[decltype(i_)::value] = 0; });
         gl::static_for<0, NZ>([&](auto ja_) {
             constexpr int ja = decltype(ja_)::value;
-            const uint64_t idx = src.index(nat0 + t + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
+            const uint64_t idx = src.index(L + ((static_cast<uint64_t>(ja) * B + jb) << sh), nmask);
             v[gl::bitrev_c(ja, LA)] = src.finish(idx, raw[ja]);
         });
         gl::dit_pow2_sparse<LA, ew_log<LA>(), prefix_mask(NZ, LA)>(v);
@@ -230,7 +256,9 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
         const uint32_t plane = PL == 2 ? (pc & 1) : 0, t = PL == 2 ? (pc >> 1) : pc;
         uint64_t v[B];
         unpark<LB>(s, v, pc, ka, PW, pitch);
-        const uint64_t out0 = ((row0 + (static_cast<uint64_t>(t) << mid_bits)) << RB) + ka;
+        const uint64_t orow =
+            rot ? gather_row((nat0 + t + rot) & lmask, d, mid_bits) : row0 + (static_cast<uint64_t>(t) << mid_bits);
+        const uint64_t out0 = (orow << RB) + ka;
         gl::static_for<0, B>([&](auto kb_) {
             constexpr int kb = decltype(kb_)::value;
             y[PL * (out0 + A * kb) + plane] = v[kb];
