@@ -322,6 +322,55 @@ def commit_tree(b, wl: Workload, reps: int = 10) -> dict:
             "achieved_gbs": round(matrix / ms / 1e6, 1), "reps": reps}
 
 
+# The reference's two production commitments and its A100 times for them
+# (benchmarks/results/c3-table-a100-2026-07-17-5a2edbe.json, pcs_commitments[0|1].commit_s).
+REFERENCE_COMMITS = (
+    ("weights", 24576, 13, 512, 15, 0x51, 0.148233502),
+    ("embed", 2080, 15, 512, 17, 0x52, 0.05474647),
+)
+
+
+def reference_commits(b, reps: int = 5) -> dict:
+    """C3_WEIGHTS and C3_EMBED committed as the reference's report commits
+    them (rust/volta-bench/src/bin/p6_report.rs:2584-2635, 2929-2972): the
+    layouts' tensors resident as separate buffers, then
+    commit_resident_from_device with one strided placement per tensor (48 for
+    the weights, wte and wpe for the embedding) -- zero the packed target,
+    place, ChaCha8 pads, messages, NTT, BLAKE3 column tree, root read back.
+    Wall time around the whole call, median of `reps` after one warm-up, next
+    to the reference's A100 time for the same commitment (not part of
+    `value`)."""
+    from volta_mi355x import ligero
+    from volta_mi355x import workloads as W
+    out = {}
+    for name, rows, col_bits, pad, code_bits, seed_byte, ref_s in REFERENCE_COMMITS:
+        slots, total = W.c3_weights_slots() if name == "weights" else W.c3_embed_slots()
+        params = ligero.LigeroParams(rows=rows, col_bits=col_bits, pad=pad, code_bits=code_bits)
+        assert total == params.rows * params.cols
+        sources = [b.upload_device(W.slot_tensor(f"volta-mi355x/{name}", s_).reshape(-1)) for s_ in slots]
+        placements = [ligero.ResidentWeightPlacement(src, 0, s_.k, s_.n, s_.offset, s_.stride, total)
+                      for src, s_ in zip(sources, slots)]
+        times, root = [], b""
+        for i in range(reps + 1):
+            b.synchronize()
+            t0 = time.perf_counter()
+            root, pm = ligero.commit_resident_from_device(b, placements, params, bytes([seed_byte]) * 32)
+            dt = time.perf_counter() - t0
+            ligero.free_resident_matrix(b, pm)
+            if i:
+                times.append(dt)
+        for src in sources:
+            b.free_device(src)
+        t = statistics.median(times)
+        out[name] = {"rows": rows, "cols": params.cols, "pad": pad, "code_len": params.code_len,
+                     "tensors": len(slots), "ms_per_commit": round(t * 1e3, 3),
+                     "gelem_per_s": round(rows * params.code_len / t / 1e9, 2), "root": root.hex(),
+                     "reference_a100_ms": round(ref_s * 1e3, 2), "speedup_vs_reference_a100": round(ref_s / t, 1)}
+    out["reference_source"] = "benchmarks/results/c3-table-a100-2026-07-17-5a2edbe.json pcs_commitments[].commit_s"
+    out["reps"] = reps
+    return out
+
+
 def x4_transforms(b, log_n: int = 24, reps: int = 10) -> dict:
     """The X4 extension-field transforms (not part of `value`): the rate-1/8
     encode NTT of 2^(log_n - 3) Fp2 coefficients into 2^log_n points
@@ -448,6 +497,7 @@ def main() -> int:
     ap.add_argument("--no-commit-tree", action="store_true")
     ap.add_argument("--no-x4", action="store_true")
     ap.add_argument("--no-seam-chain", action="store_true")
+    ap.add_argument("--no-reference-commits", action="store_true")
     ap.add_argument("--x4-log-n", type=int, default=24)
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -491,10 +541,14 @@ def main() -> int:
     if not a.no_seam_chain:
         log("seam chain (messages + NTT through the reference's calls)")
         chain_leg = seam_chain(b, wl)
+    wl_close = wl.close
+    commits = None
+    if not a.no_reference_commits:
+        log("the reference's production commitments (C3_WEIGHTS, C3_EMBED)")
+        commits = reference_commits(b)
     copy_gbs = None if a.no_copy_probe else round(copy_bandwidth(b), 1)
     expand_gbs = None if a.no_copy_probe else round(expand_bandwidth(b), 1)
     chain = None if a.no_copy_probe else fp2_chain_peak(b)
-    wl_close = wl.close
     cpu = None
     if not a.no_cpu_baseline:
         log("cpu baseline")
@@ -537,6 +591,7 @@ def main() -> int:
         "seam_chain": chain_leg,
         "commit_tree": tree,
         "x4": x4,
+        "reference_commits": commits,
     }
     print(json.dumps(out), flush=True)
     return 0

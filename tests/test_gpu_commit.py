@@ -201,3 +201,41 @@ def test_resident_opening_steps_match_oracle(backend, oracle, rows, col_bits, pa
                 assert np.array_equal(np.asarray(got[k]), np.asarray(v)), k
     finally:
         ligero.free_resident_matrix(backend, pm)
+
+
+@pytest.mark.parametrize("name", ["embed", "weights"])
+def test_reference_production_commitments(oracle, name):
+    """C3_EMBED (2 tensors) and C3_WEIGHTS (48 tensors) in the reference's own
+    layouts, committed as its report commits them (p6_report.rs:2584-2615,
+    2929-2952): each tensor a resident buffer, one strided placement per
+    tensor, pad 512, the seeds 0x51/0x52.  The root equals the oracle's CPU
+    commit of the packed matrix, and the stats carry exactly the placements'
+    bytes."""
+    from volta_mi355x import Backend, ligero, workloads as W
+    slots, total = W.c3_weights_slots() if name == "weights" else W.c3_embed_slots()
+    rows, col_bits, code_bits = (24576, 13, 15) if name == "weights" else (2080, 15, 17)
+    params = ligero.LigeroParams(rows=rows, col_bits=col_bits, pad=512, code_bits=code_bits)
+    seed = bytes([0x51 if name == "weights" else 0x52]) * 32
+    g = np.random.Generator(np.random.PCG64(rows))
+    tensors = [g.integers(-(1 << 15), 1 << 15, size=(s.k, s.n), dtype=np.int16) for s in slots]
+    tensors[0].reshape(-1)[:2] = [-32768, 32767]
+    packed = np.zeros(total, np.int16)
+    for t, s in zip(tensors, slots):
+        packed[s.offset:s.offset + s.k * s.stride].reshape(s.k, s.stride)[:, :s.n] = t
+    with Backend() as b:
+        base = b.memory_breakdown()[1]
+        sources = [b.upload_device(t.reshape(-1)) for t in tensors]
+        placements = [ligero.ResidentWeightPlacement(src, 0, s.k, s.n, s.offset, s.stride, total)
+                      for src, s in zip(sources, slots)]
+        b.reset_stats()
+        root, pm = ligero.commit_resident_from_device(b, placements, params, seed)
+        st = b.get_stats()
+        ligero.free_resident_matrix(b, pm)
+        for src in sources:
+            b.free_device(src)
+        assert b.memory_breakdown()[1] == base
+    del tensors
+    assert st["d2d_bytes"] == sum(s.k * s.n for s in slots) * 2
+    assert st["device_zeroed_bytes"] == total * 2
+    assert st["device_generated_bytes"] == rows * 512 * 8
+    assert root == oracle.commit_root(packed, rows, params.cols, 512, params.code_len, seed)

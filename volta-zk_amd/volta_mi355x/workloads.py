@@ -145,3 +145,72 @@ def challenges_fp2(label: str, count: int) -> np.ndarray:
 
 def c5_query_columns(n: int = 1 << 24, queries: int = 256) -> np.ndarray:
     return rng("volta-mi355x/c5/queries").integers(0, n, size=queries, dtype=np.uint32)
+
+
+# ---- the reference's production commitment layouts ---------------------------------------------
+
+@dataclass(frozen=True)
+class TensorSlot:
+    """One tensor's block in a commitment (rust/volta-pcs/src/layer_layout.rs
+    TensorSlot): k rows of n i16 placed from ``offset`` with row stride
+    ``stride`` (n rounded up to a power of two), inside a k_pad x n_pad block."""
+    name: str
+    k: int
+    n: int
+    offset: int
+    stride: int
+
+
+def block_layout(shapes, pad_outer: bool = True):
+    """LayerWeightLayout2::for_shapes(_exact) (layer_layout.rs:221-253): each
+    (k, n) tensor gets a k_pad x n_pad block (next powers of two); blocks are
+    placed largest first (ties in input order) so every offset is a multiple
+    of its block; the total is the end of the last block, rounded up to a
+    power of two unless ``pad_outer`` is false.  Returns (slots in input
+    order, total)."""
+    blocks = [(name, k, n, _pow2(k) * _pow2(n)) for name, k, n in shapes]
+    order = sorted(range(len(blocks)), key=lambda i: -blocks[i][3])  # sorted() is stable
+    offsets, cursor = {}, 0
+    for i in order:
+        offsets[i] = cursor
+        cursor += blocks[i][3]
+    total = _pow2(cursor) if pad_outer else cursor
+    slots = [TensorSlot(name, k, n, offsets[i], _pow2(n)) for i, (name, k, n, _) in enumerate(blocks)]
+    assert all(s.offset % (_pow2(s.k) * _pow2(s.n)) == 0 for s in slots)
+    return slots, total
+
+
+def _pow2(x: int) -> int:
+    return 1 << (x - 1).bit_length()
+
+
+# One GPT-2-small layer (layout_gpt2_layer, layer_layout.rs:122-143): c_attn on
+# its permuted 768 x 4096 column layout, attn_proj, ffn_up, ffn_down.
+GPT2_LAYER_SHAPES = (("c_attn", 768, 4096), ("attn_proj", 768, 768), ("ffn_up", 768, 3072),
+                     ("ffn_down", 3072, 768))
+
+
+def c3_weights_slots():
+    """The consolidated weights commitment (layout_gpt2_weights_c3,
+    layer_layout.rs:170-178; C3_WEIGHTS = 24,576 x 2^13, layer_layout.rs:30):
+    twelve 2^24-coefficient layer blocks, the layer layout inside each.  The
+    reference's report commits these 48 tensors by strided device placements
+    (rust/volta-bench/src/bin/p6_report.rs:2584-2615)."""
+    layer, total = block_layout(GPT2_LAYER_SHAPES)
+    assert total == 1 << 24
+    slots = [TensorSlot(f"h{l}.{s.name}", s.k, s.n, l * total + s.offset, s.stride)
+             for l in range(12) for s in layer]
+    return slots, 12 * total
+
+
+def c3_embed_slots():
+    """The exact-block embedding commitment (layout_gpt2_embed_c3,
+    layer_layout.rs:209-214; C3_EMBED = 2,080 x 2^15, layer_layout.rs:34): wte
+    50,257 x 768 and wpe 1,024 x 768 without the outer 2^27 pad
+    (p6_report.rs:2929-2952)."""
+    return block_layout((("wte", 50257, 768), ("wpe", 1024, 768)), pad_outer=False)
+
+
+def slot_tensor(label: str, slot: TensorSlot) -> np.ndarray:
+    """Gaussian i16 weights for one tensor (k x n), seeded by label and name."""
+    return gaussian_i16(f"{label}/{slot.name}", slot.k * slot.n).reshape(slot.k, slot.n)
