@@ -324,9 +324,10 @@ def commit_tree(b, wl: Workload, reps: int = 10) -> dict:
 
 # The reference's two production commitments and its A100 times for them
 # (benchmarks/results/c3-table-a100-2026-07-17-5a2edbe.json, pcs_commitments[0|1].commit_s).
+# name, rows, col_bits, pad, code_bits, pad-seed byte, commit_s, open_s, claims per tensor
 REFERENCE_COMMITS = (
-    ("weights", 24576, 13, 512, 15, 0x51, 0.148233502),
-    ("embed", 2080, 15, 512, 17, 0x52, 0.05474647),
+    ("weights", 24576, 13, 512, 15, 0x51, 0.148233502, 0.266512943, (2,) * 48),
+    ("embed", 2080, 15, 512, 17, 0x52, 0.05474647, 0.027055026, (4, 2)),
 )
 
 
@@ -337,35 +338,65 @@ def reference_commits(b, reps: int = 5) -> dict:
     commit_resident_from_device with one strided placement per tensor (48 for
     the weights, wte and wpe for the embedding) -- zero the packed target,
     place, ChaCha8 pads, messages, NTT, BLAKE3 column tree, root read back.
-    Wall time around the whole call, median of `reps` after one warm-up, next
-    to the reference's A100 time for the same commitment (not part of
-    `value`)."""
+    Then the device side of the resident opening (open_multi_zk_resident,
+    ligero.rs:1216-1551) with as many block claims as the report makes (96 =
+    two per weight tensor; 6 = four on wte, two on wpe, model_proof.rs:2185,
+    2366-2367), random claim points and 120 queries: masks and their tree,
+    the proximity pass, the block-claim pass, the mask dots, the query
+    columns and paths, all read back.  Wall time around each call, median of
+    `reps` after one warm-up, next to the reference's A100 times for the same
+    commitment and opening (not part of `value`; the reference's opening time
+    also holds its transcript and proof assembly on the host)."""
+    import numpy as np
+
     from volta_mi355x import ligero
     from volta_mi355x import workloads as W
+    P = W.P
+    _pow2 = W._pow2
     out = {}
-    for name, rows, col_bits, pad, code_bits, seed_byte, ref_s in REFERENCE_COMMITS:
+    for name, rows, col_bits, pad, code_bits, seed_byte, ref_s, ref_open_s, per_tensor in REFERENCE_COMMITS:
         slots, total = W.c3_weights_slots() if name == "weights" else W.c3_embed_slots()
         params = ligero.LigeroParams(rows=rows, col_bits=col_bits, pad=pad, code_bits=code_bits)
         assert total == params.rows * params.cols
         sources = [b.upload_device(W.slot_tensor(f"volta-mi355x/{name}", s_).reshape(-1)) for s_ in slots]
         placements = [ligero.ResidentWeightPlacement(src, 0, s_.k, s_.n, s_.offset, s_.stride, total)
                       for src, s_ in zip(sources, slots)]
-        times, root = [], b""
+        times, root, pm = [], b"", None
         for i in range(reps + 1):
+            if pm is not None:
+                ligero.free_resident_matrix(b, pm)
             b.synchronize()
             t0 = time.perf_counter()
             root, pm = ligero.commit_resident_from_device(b, placements, params, bytes([seed_byte]) * 32)
             dt = time.perf_counter() - t0
-            ligero.free_resident_matrix(b, pm)
             if i:
                 times.append(dt)
         for src in sources:
             b.free_device(src)
         t = statistics.median(times)
+        g = np.random.Generator(np.random.PCG64(rows))
+        claims = [(s_.offset, g.integers(0, P, size=((_pow2(s_.k) * _pow2(s_.n)).bit_length() - 1, 2),
+                                         dtype=np.uint64))
+                  for s_, count in zip(slots, per_tensor) for _ in range(count)]
+        c = tuple(int(x) for x in g.integers(0, P, size=2, dtype=np.uint64))
+        js = g.integers(0, params.code_len, size=120, dtype=np.uint32)
+        open_times = []
+        for i in range(reps + 1):
+            b.synchronize()
+            t0 = time.perf_counter()
+            ligero.open_rows_resident(b, pm, claims, c, js, bytes([seed_byte ^ 0xFF]) * 32)
+            dt = time.perf_counter() - t0
+            if i:
+                open_times.append(dt)
+        ligero.free_resident_matrix(b, pm)
+        to = statistics.median(open_times)
         out[name] = {"rows": rows, "cols": params.cols, "pad": pad, "code_len": params.code_len,
                      "tensors": len(slots), "ms_per_commit": round(t * 1e3, 3),
                      "gelem_per_s": round(rows * params.code_len / t / 1e9, 2), "root": root.hex(),
-                     "reference_a100_ms": round(ref_s * 1e3, 2), "speedup_vs_reference_a100": round(ref_s / t, 1)}
+                     "reference_a100_ms": round(ref_s * 1e3, 2), "speedup_vs_reference_a100": round(ref_s / t, 1),
+                     "claims": len(claims), "queries": 120, "ms_per_open": round(to * 1e3, 3),
+                     "reference_a100_open_ms": round(ref_open_s * 1e3, 2),
+                     "open_speedup_vs_reference_a100": round(ref_open_s / to, 1)}
     out["reference_source"] = "benchmarks/results/c3-table-a100-2026-07-17-5a2edbe.json pcs_commitments[].commit_s"
     out["reps"] = reps
     return out

@@ -45,6 +45,55 @@ def test_combine_rows_device_matches_oracle(backend, oracle, rows, cols, pad, co
     assert (got == oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)).all()
 
 
+def block_sparse_coefficients(seed, rows, comb):
+    """Coefficients as an opening's block claims make them: zero outside a
+    block of rows, plus the cases the zero-chunk skip must get right."""
+    g = np.random.Generator(np.random.PCG64(seed))
+    co = np.zeros((comb, rows, 2), np.uint64)
+    # 0: all zero; 1: one aligned block; 2: a block across chunk boundaries;
+    # 3: a pair of rows whose coefficients sum to 0 mod p, and a far row;
+    # the rest dense
+    co[1, 64:96] = g.integers(0, P, size=(32, 2), dtype=np.uint64)
+    co[2, 100:300] = g.integers(0, P, size=(200, 2), dtype=np.uint64)
+    c = g.integers(1, P, size=2, dtype=np.uint64)
+    co[3, 5], co[3, 6] = c, np.uint64(P) - c
+    co[3, rows - 1] = g.integers(0, P, size=2, dtype=np.uint64)
+    co[4:] = g.integers(0, P, size=(comb - 4, rows, 2), dtype=np.uint64)
+    return co.reshape(comb * rows, 2)
+
+
+@pytest.mark.parametrize("rows,cols,pad,comb", [(4096, 2048, 512, 7), (4096, 2048, 0, 6), (512, 256, 8, 7),
+                                               (320, 64, 3, 5)])
+def test_combine_rows_with_zero_coefficient_chunks(backend, oracle, rows, cols, pad, comb):
+    """Block-claim coefficients (zero outside a block): chunks whose
+    coefficients are all zero are skipped, a chunk whose nonzero coefficients
+    sum to 0 mod p is not, odd and even combination counts; through the
+    allocating and the allocation-free entry points."""
+    from volta_mi355x import FP2
+    w = rand_i16(rows * comb, rows * cols)
+    pads = rand_fp(rows + pad, rows * pad) if pad else np.zeros(1, np.uint64)
+    co = block_sparse_coefficients(rows + comb, rows, comb)
+    dw, dp, dc = backend.upload_device(w), backend.upload_device(pads), backend.upload_device(co, FP2)
+    want = oracle.pcs_combine_rows(w, pads if pad else None, co, rows, cols, pad, comb)
+    assert not want[0].any() and want[3].any()
+    out = backend.pcs_combine_rows_device(dw, 0, dp, 0, dc, 0, rows, cols, pad, comb)
+    got = backend.download_device(out).view(np.uint64).reshape(comb, cols + pad, 2)
+    assert (got == want).all()
+    # the allocation-free entry, twice: its scratch holds the previous call's
+    # partials (the two 4096-row shapes need more partials than it holds)
+    out2 = backend.alloc_device(comb * (cols + pad), FP2)
+    for _ in range(2):
+        rc = backend.lib.volta_mi355x_pcs_combine_rows_device_noalloc(
+            backend.raw, dw.id, 0, dp.id, 0, dc.id, 0, rows, cols, pad, comb, out2.id, 0)
+        if rows == 4096:
+            assert rc != 0 and "scratch" in backend.last_error()
+        else:
+            assert rc == 0, backend.last_error()
+            assert (backend.download_device(out2).view(np.uint64).reshape(comb, cols + pad, 2) == want).all()
+    for b in (dw, dp, dc, out, out2):
+        backend.free_device(b)
+
+
 def test_combine_rows_host_entry_point(backend, oracle):
     rows, cols, pad, comb = 33, 40, 6, 2
     w = rand_i16(1, rows * cols)
@@ -330,7 +379,8 @@ def test_coarse_timing_scope_and_wall_only_policy():
 
 # ---- opening-path helpers ----------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,dims", [(1, 0), (3, 1), (2, 3), (4, 4), (5, 7), (2, 12), (1, 18)])
+@pytest.mark.parametrize("rows,dims", [(1, 0), (3, 1), (2, 3), (4, 4), (5, 7), (2, 12), (1, 18), (1, 5), (1, 9),
+                                       (1, 11), (7, 6), (96, 13)])
 def test_eq_rows_match_oracle(backend, oracle, rows, dims):
     from volta_mi355x import FP2
     pts = rand_fp(rows * 100 + dims, (rows * dims, 2)) if dims else None

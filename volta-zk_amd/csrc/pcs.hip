@@ -51,9 +51,11 @@ int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows
 // rust/volta-pcs/src/ligero.rs:1114-1135; coefficient layout combinations x
 // rows, rust/volta-accel/src/lib.rs:6522-6569).  Unlike the reference kernel,
 // which re-reads the matrix once per (combination, column) thread, the matrix
-// is read once: each workgroup owns a chunk of rows x a tile of columns,
-// accumulates all combinations lazily, and writes one partial per chunk; a
-// second kernel sums partials mod p.
+// is read once per pair of combinations: each workgroup owns a chunk of rows x
+// a tile of columns, accumulates two combinations lazily, and writes one
+// partial per chunk; a second kernel sums partials mod p.  A chunk whose
+// coefficients are zero for the pair is not read at all (an opening's block
+// claims weight only their own block's rows).
 //
 // i16 data: with w' = w + 2^15 in [0, 2^16) and a coefficient component
 // x = xh*2^32 + xl, sum_i x_i w_i = sum xl_i w'_i + 2^32 sum xh_i w'_i
@@ -76,8 +78,13 @@ constexpr int CI_UNROLL = 8;        // row loads kept in flight per thread
 
 // S[ck][comb][h] = sum over the chunk's rows of component h of coeff[comb][i]
 // (mod p): the 2^15 bias correction of the offset-binary trick below.
-__global__ __launch_bounds__(256) void coeff_chunk_sums(const Fp2* coeffs, uint64_t* sums, size_t rows,
-                                                        size_t chunk) {
+// nz[ck][comb] = 1 when any coefficient of the chunk is nonzero: the exact
+// sums of the 32-bit halves are zero only then (a nonzero chunk can sum to
+// 0 mod p, so the field sums cannot tell).  A block claim's equality weights
+// cover only the rows of its block, so most (chunk, combination) pairs of an
+// opening are zero and skip their share of the matrix.
+__global__ __launch_bounds__(256) void coeff_chunk_sums(const Fp2* coeffs, uint64_t* sums, uint32_t* nz,
+                                                        size_t rows, size_t chunk) {
     __shared__ uint64_t red[4][256];
     const size_t ck = blockIdx.x, comb = blockIdx.y, combinations = gridDim.y;
     const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
@@ -104,6 +111,7 @@ __global__ __launch_bounds__(256) void coeff_chunk_sums(const Fp2* coeffs, uint6
         // chunk <= 2^16 rows keeps each half-sum below 2^48
         sums[(ck * combinations + comb) * 2 + 0] = gl::add(gl::canon(red[0][0]), gl::mul(gl::canon(red[1][0]), two32));
         sums[(ck * combinations + comb) * 2 + 1] = gl::add(gl::canon(red[2][0]), gl::mul(gl::canon(red[3][0]), two32));
+        nz[ck * combinations + comb] = (red[0][0] | red[1][0] | red[2][0] | red[3][0]) != 0;
     }
 }
 
@@ -113,17 +121,35 @@ __global__ __launch_bounds__(256) void coeff_chunk_sums(const Fp2* coeffs, uint6
 // x = xh*2^32 + xl, sum_i x_i w_i = sum xl_i w'_i + 2^32 sum xh_i w'_i
 // - 2^15 sum_i x_i.  Each 32x16-bit product is < 2^48, so u64 accumulators
 // absorb up to 2^16 rows exactly; the fold to a field element happens once.
+// Combinations comb_base + KC z .. + KC - 1 for z = blockIdx.z.  A chunk whose
+// coefficients are all zero for these combinations (nz) reads no matrix row:
+// it writes zeros when its partials are the output (one chunk), and nothing
+// otherwise (reduce_partials skips it).
 template <int KC>
 __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_t* w, const Fp2* coeffs,
-                                                                   const uint64_t* sums, Fp2* partials,
-                                                                   size_t rows, size_t cols, size_t msg_len,
-                                                                   size_t comb0, size_t combinations, size_t chunk,
-                                                                   int vec_ok) {
+                                                                   const uint64_t* sums, const uint32_t* nz,
+                                                                   Fp2* partials, size_t rows, size_t cols,
+                                                                   size_t msg_len, size_t comb_base,
+                                                                   size_t combinations, size_t chunk, int vec_ok,
+                                                                   int direct) {
     __shared__ Fp2 red[CI_WAVES - 1][KC][CI_COLS][64];
     // the wave index is uniform: row bounds and coefficient addresses stay scalar (SMEM loads)
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const size_t j0 = (static_cast<size_t>(blockIdx.x) * 64 + lane) * CI_COLS;
     const size_t ck = blockIdx.y;
+    const size_t comb0 = comb_base + static_cast<size_t>(KC) * blockIdx.z;
+    uint32_t any = 0;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) any |= nz[ck * combinations + comb0 + k];
+    if (!any) {  // uniform over the workgroup
+        if (!direct || wave > 0) return;
+#pragma unroll
+        for (int k = 0; k < KC; ++k)
+#pragma unroll
+            for (int q = 0; q < CI_COLS; ++q)
+                if (j0 + q < cols) partials[(ck * combinations + comb0 + k) * msg_len + j0 + q] = Fp2{0, 0};
+        return;
+    }
     const size_t c0 = ck * chunk, c1 = min(rows, c0 + chunk);
     const size_t per = (c1 - c0 + CI_WAVES - 1) / CI_WAVES;
     const size_t r0 = min(c1, c0 + wave * per), r1 = min(c1, r0 + per);
@@ -201,7 +227,6 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
     if (wave > 0) return;
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
-        if (comb0 + k >= combinations) break;
         // the offset-binary bias of the whole chunk: 2^15 sum_i x_i
         uint64_t bias[2];
 #pragma unroll
@@ -219,15 +244,36 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
 }
 
 // Pad columns j in [cols, cols+pad): full field products.
-__global__ void combine_pads_partial(const uint64_t* pads, const Fp2* coeffs, Fp2* partials, size_t rows,
-                                     size_t cols, size_t pad, size_t msg_len, size_t combinations, size_t chunk) {
+constexpr int PAD_UNROLL = 8;
+
+__global__ void combine_pads_partial(const uint64_t* pads, const Fp2* coeffs, const uint32_t* nz, Fp2* partials,
+                                     size_t rows, size_t cols, size_t pad, size_t msg_len, size_t combinations,
+                                     size_t chunk, int direct) {
     const size_t p = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const size_t comb = blockIdx.z;
     if (p >= pad) return;
     const size_t ck = blockIdx.y;
+    if (!nz[ck * combinations + comb]) {  // zero coefficients: as combine_i16_partial
+        if (direct) partials[(ck * combinations + comb) * msg_len + cols + p] = Fp2{0, 0};
+        return;
+    }
     const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
+    const Fp2* cf = coeffs + comb * rows;
     Fp2 acc{0, 0};
-    for (size_t i = r0; i < r1; ++i) acc = gl::fp2_add(acc, gl::fp2_mul_base(coeffs[comb * rows + i], pads[i * pad + p]));
+    size_t i = r0;
+    // PAD_UNROLL rows' coefficient and pad loads in flight before their products
+    for (; i + PAD_UNROLL <= r1; i += PAD_UNROLL) {
+        Fp2 cv[PAD_UNROLL];
+        uint64_t pv[PAD_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PAD_UNROLL; ++u) {
+            cv[u] = cf[i + u];
+            pv[u] = pads[(i + u) * pad + p];
+        }
+#pragma unroll
+        for (int u = 0; u < PAD_UNROLL; ++u) acc = gl::fp2_add(acc, gl::fp2_mul_base(cv[u], pv[u]));
+    }
+    for (; i < r1; ++i) acc = gl::fp2_add(acc, gl::fp2_mul_base(cf[i], pads[i * pad + p]));
     partials[(ck * combinations + comb) * msg_len + cols + p] = acc;
 }
 
@@ -293,14 +339,20 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_fp_partial(const uint64_
 constexpr int RED_Z = 64;
 constexpr int RED_LANES = 16;
 
+// With nz (combinations x msg_len outputs per chunk), a chunk whose flag for
+// the output's combination is 0 has no partial and is skipped.
 __global__ __launch_bounds__(RED_Z * RED_LANES) void reduce_partials(const Fp2* partials, Fp2* out, size_t chunks,
-                                                                     size_t per_chunk) {
+                                                                     size_t per_chunk, const uint32_t* nz,
+                                                                     size_t combinations, size_t msg_len) {
     __shared__ Fp2 red[RED_LANES][RED_Z];
     const int tz = threadIdx.x % RED_Z, tl = threadIdx.x / RED_Z;
     const size_t z = static_cast<size_t>(blockIdx.x) * RED_Z + tz;
     Fp2 acc{0, 0};
-    if (z < per_chunk)
-        for (size_t ck = tl; ck < chunks; ck += RED_LANES) acc = gl::fp2_add(acc, partials[ck * per_chunk + z]);
+    if (z < per_chunk) {
+        const size_t comb = nz ? z / msg_len : 0;
+        for (size_t ck = tl; ck < chunks; ck += RED_LANES)
+            if (!nz || nz[ck * combinations + comb]) acc = gl::fp2_add(acc, partials[ck * per_chunk + z]);
+    }
     red[tl][tz] = acc;
     __syncthreads();
     for (int w = RED_LANES / 2; w > 0; w >>= 1) {
@@ -332,7 +384,7 @@ static size_t comb_chunk(size_t rows, size_t col_blocks, size_t largest = COMB_C
 
 // The i16 combination's launch plan: rows per partial chunk and the bytes of
 // the per-chunk partials (none for one chunk: it writes out directly) and of
-// the chunks' coefficient sums.
+// the chunks' coefficient sums followed by their nonzero flags.
 struct CombinePlan {
     size_t msg_len, col_blocks, chunk, chunks, per_chunk, part_bytes, sum_bytes;
 };
@@ -344,7 +396,7 @@ static int combine_plan(Context* c, size_t rows, size_t cols, size_t pad, size_t
     p->chunks = (rows + p->chunk - 1) / p->chunk;
     size_t bytes = 0;
     if (!mul_ok(combinations, p->msg_len, &p->per_chunk) || !mul_ok(p->per_chunk * sizeof(Fp2), p->chunks, &bytes) ||
-        !mul_ok(p->chunks * combinations, 2 * sizeof(uint64_t), &p->sum_bytes))
+        !mul_ok(p->chunks * combinations, 2 * sizeof(uint64_t) + sizeof(uint32_t), &p->sum_bytes))
         return fail_msg(c, "PCS combination partials overflow size_t");
     if (p->chunks > 65535 || combinations > 65535)
         return fail_msg(c, "PCS combination row or combination count exceeds the supported maximum");
@@ -352,44 +404,50 @@ static int combine_plan(Context* c, size_t rows, size_t cols, size_t pad, size_t
     return 0;
 }
 
-// Every partial and every coefficient sum the kernels read is written earlier
-// in the same call (each (chunk, combination, column) exactly once), so the
-// buffers need no clearing.
+// The coefficient sums and flags are written first in the same call; a
+// partial is written for every (chunk, combination) the flags mark nonzero
+// (and for all of them when the partials are the output), and the reduction
+// reads exactly those, so the buffers need no clearing.
 static int combine_launch(Context* c, const int16_t* w, const uint64_t* pads, const Fp2* coeffs, size_t rows,
                           size_t cols, size_t pad, size_t combinations, Fp2* out, const CombinePlan& pl, Fp2* part,
                           uint64_t* sums) {
     const size_t chunk = pl.chunk, chunks = pl.chunks, msg_len = pl.msg_len;
-    if (chunks == 1) part = out;  // one chunk: the partials are the result
+    uint32_t* nz = reinterpret_cast<uint32_t*>(sums + chunks * combinations * 2);
+    const int direct = chunks == 1;
+    if (direct) part = out;  // one chunk: the partials are the result
     hipLaunchKernelGGL(coeff_chunk_sums, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(combinations)),
-                       dim3(256), 0, c->stream, coeffs, sums, rows, chunk);
+                       dim3(256), 0, c->stream, coeffs, sums, nz, rows, chunk);
     VMX_HIP(c, hipGetLastError());
-    const dim3 grid(static_cast<unsigned>(pl.col_blocks), static_cast<unsigned>(chunks));
     // Vector row loads need a base and a row pitch aligned to CI_COLS i16.
     const int vec_ok = (reinterpret_cast<uintptr_t>(w) % (2 * CI_COLS) == 0) && (cols % CI_COLS == 0);
-    if (launch_comb_groups(combinations, [&](size_t c0, int kc) {
-            if (kc == 2)
-                hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
-                                   static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
-                                   chunk, vec_ok);
-            else
-                hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
-                                   static_cast<const uint64_t*>(sums), part, rows, cols, msg_len, c0, combinations,
-                                   chunk, vec_ok);
-            VMX_HIP(c, hipGetLastError());
-            return 0;
-        }))
-        return -1;
+    const size_t pairs = combinations / 2;
+    if (pairs) {  // every pair of combinations in one launch
+        const dim3 grid(static_cast<unsigned>(pl.col_blocks), static_cast<unsigned>(chunks),
+                        static_cast<unsigned>(pairs));
+        hipLaunchKernelGGL(combine_i16_partial<2>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
+                           static_cast<const uint64_t*>(sums), static_cast<const uint32_t*>(nz), part, rows, cols,
+                           msg_len, size_t{0}, combinations, chunk, vec_ok, direct);
+        VMX_HIP(c, hipGetLastError());
+    }
+    if (combinations & 1) {  // the last, odd one
+        const dim3 grid(static_cast<unsigned>(pl.col_blocks), static_cast<unsigned>(chunks), 1u);
+        hipLaunchKernelGGL(combine_i16_partial<1>, grid, dim3(COMB_THREADS), 0, c->stream, w, coeffs,
+                           static_cast<const uint64_t*>(sums), static_cast<const uint32_t*>(nz), part, rows, cols,
+                           msg_len, combinations - 1, combinations, chunk, vec_ok, direct);
+        VMX_HIP(c, hipGetLastError());
+    }
     if (pad) {
         const dim3 g(static_cast<unsigned>((pad + 255) / 256), static_cast<unsigned>(chunks),
                      static_cast<unsigned>(combinations));
-        hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs, part, rows, cols, pad,
-                           msg_len, combinations, chunk);
+        hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs,
+                           static_cast<const uint32_t*>(nz), part, rows, cols, pad, msg_len, combinations, chunk,
+                           direct);
         VMX_HIP(c, hipGetLastError());
     }
-    if (chunks == 1) return 0;
+    if (direct) return 0;
     hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((pl.per_chunk + RED_Z - 1) / RED_Z)),
                        dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks,
-                       pl.per_chunk);
+                       pl.per_chunk, static_cast<const uint32_t*>(nz), combinations, msg_len);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
@@ -477,7 +535,8 @@ int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, con
         return -1;
     if (chunks == 1) return 0;
     hipLaunchKernelGGL(reduce_partials, dim3(static_cast<unsigned>((per_chunk + RED_Z - 1) / RED_Z)),
-                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk);
+                       dim3(RED_Z * RED_LANES), 0, c->stream, static_cast<const Fp2*>(part), out, chunks, per_chunk,
+                       static_cast<const uint32_t*>(nullptr), size_t{0}, size_t{1});
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
@@ -816,7 +875,11 @@ __global__ __launch_bounds__(DOT_THREADS) void fp2_row_dots_kernel(const Fp2* __
 
 int eq_rows(Context* c, const Fp2* points, size_t rows, size_t dims, Fp2* out) {
     const int d = static_cast<int>(dims);
-    const int low = d < 4 ? d : 4;
+    // Up to 16 outputs per thread, fewer when that would leave under 256
+    // threads (a single block claim's 2^9 weights: 256 threads of two,
+    // instead of 32 threads of sixteen running one serial wave).
+    int low = d < 4 ? d : 4;
+    while (low > 0 && (rows << (dims - low)) < 256) --low;
     const size_t threads = rows << (dims - low);
     const dim3 grid(grid_for(threads, 256, 1 << 16));
     switch (low) {
