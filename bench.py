@@ -454,7 +454,12 @@ def x4_transforms(b, log_n: int = 24, reps: int = 10) -> dict:
 
 def cpu_baseline(name: str, wl: Workload) -> dict:
     """The oracle's restatement of the reference CPU path (per-row radix-2 DIT
-    NttPlan::forward + combine_rows), OpenMP over this host's cores."""
+    NttPlan::forward, combine_rows with its column chunks), OpenMP over this
+    host's cores, on a bounded sample of the configuration's rows (about 6 s a
+    run): the same step as the GPU's over those rows, median of 3 after one
+    warm-up, scaled to codeword elements per second.  C5 times its forward and
+    inverse transforms and the combination over a subset of its rows, one
+    2^24-point transform per core, twice."""
     import numpy as np
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
@@ -462,23 +467,72 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
     from volta_mi355x import workloads as W
     cfg = W.CONFIGS[name]
     threads = oracle.default_threads()
-    if name not in ("c2", "c3"):
+    rows_all, n = cfg.rows, cfg.n
+
+    if name in ("c2", "c3"):
+        w = wl.host_w
+        co = np.concatenate([oracle.fp2_powers(tuple(int(x) for x in c), cfg.rows) for c in wl.challenges])
+
+        def run(rows):
+            oracle.pcs_encode_i16(w[:rows].reshape(-1), None, rows, cfg.msg_len, 0, n, threads)
+            cr = np.concatenate([co[k * cfg.rows:k * cfg.rows + rows] for k in range(cfg.combinations)])
+            oracle.pcs_combine_rows(w[:rows].reshape(-1), None, cr, rows, cfg.msg_len, 0, cfg.combinations, threads)
+        step = f"encode + {cfg.combinations} combinations"
+    elif name == "c1":
+        msgs = wl.b.download_device(wl.msgs).reshape(rows_all, cfg.msg_len)
+        co = np.zeros((rows_all, 2), np.uint64)
+        co[:, 0] = W.uniform_fp("volta-mi355x/c1/challenges", rows_all)
+
+        def run(rows):
+            oracle.ntt_encode_batch(msgs[:rows], n, threads)
+            oracle.combine_rows_fp(msgs[:rows], co[:rows], 1, threads)
+        step = "encode + 1 combination"
+    elif name == "c4":
+        cache = {}
+
+        def run(rows):
+            if rows not in cache:
+                cache[rows] = W.c4_messages(rows, cfg.msg_len)
+            oracle.ntt_encode_batch(cache[rows], n, threads)
+        step = "encode"
+    elif name in ("p15", "p17"):
+        cache = {}
+        seed = W.seed_bytes(f"volta-mi355x/{name}/pads")
+
+        def run(rows):
+            if rows not in cache:
+                cache[rows] = W.gaussian_i16(f"volta-mi355x/{name}/weights", rows * cfg.msg_len)
+            pads = oracle.fp_rows(seed, 0, rows, cfg.pad, threads)
+            oracle.pcs_encode_i16(cache[rows], pads, rows, cfg.msg_len, cfg.pad, n, threads)
+        step = "pads + encode"
+    elif name == "c5":
+        sample = min(rows_all, max(threads, 1))
+        x = W.c5_rows(sample, n)
+        c = tuple(int(v) for v in wl.challenges[0])
+        t_all = []
+        for _ in range(2):  # each run is tens of seconds: two runs, no warm-up
+            t0 = time.perf_counter()
+            fwd = oracle.ntt_forward_batch(x, threads)
+            oracle.ntt_inverse_batch(fwd, threads)
+            oracle.combine_rows_fp(fwd, oracle.fp2_powers(c, sample), 1, threads)
+            t_all.append(time.perf_counter() - t0)
+        t = statistics.median(t_all)
+        return {"value": round(2 * sample * n / t / 1e9, 4), "unit": "Gelem/s", "cores": threads,
+                "cpu_model": cpu_model(), "kind": "port",
+                "sample": f"{sample} of {rows_all} rows of c5 (forward + inverse + the combination over those rows; "
+                          f"elements counted both ways as the GPU's), mean of 2 runs without warm-up, {t:.3f} s"}
+    else:
         return None
-    w = wl.host_w
-    co = np.concatenate([oracle.fp2_powers(tuple(int(x) for x in c), cfg.rows) for c in wl.challenges])
 
-    def run(rows):
-        oracle.pcs_encode_i16(w[:rows].reshape(-1), None, rows, cfg.msg_len, 0, cfg.n, threads)
-        cr = np.concatenate([co[k * cfg.rows:k * cfg.rows + rows] for k in range(cfg.combinations)])
-        oracle.pcs_combine_rows(w[:rows].reshape(-1), None, cr, rows, cfg.msg_len, 0, cfg.combinations, threads)
-
+    probe = min(rows_all, 256 if n >= 1 << 15 else 1024)
     t0 = time.perf_counter()
-    run(min(cfg.rows, 1024))
-    per_row = (time.perf_counter() - t0) / min(cfg.rows, 1024)
-    # bounded sample: at most ~20 s of wall time over 3 timed runs
-    sample = int(min(cfg.rows, max(1024, 6.0 / max(per_row, 1e-9))))
-    sample -= sample % 1024 or 0
-    sample = max(sample, min(cfg.rows, 1024))
+    run(probe)
+    per_row = (time.perf_counter() - t0) / probe
+    # bounded sample: about 6 s a run
+    sample = int(min(rows_all, max(probe, 6.0 / max(per_row, 1e-9))))
+    sample -= sample % probe
+    sample = max(sample, probe)
+    run(sample)  # warm-up at the sample's size
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -486,13 +540,13 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {
-        "value": round(sample * cfg.n / t / 1e9, 4),
+        "value": round(sample * n / t / 1e9, 4),
         "unit": "Gelem/s",
         "cores": threads,
         "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"{sample} of {cfg.rows} rows of {name} (encode + {cfg.combinations} combinations over those rows), "
-                  f"median of 3 after 1 warmup, {t:.3f} s",
+        "sample": f"{sample} of {rows_all} rows of {name} ({step} over those rows), median of 3 after 1 warmup, "
+                  f"{t:.3f} s",
     }
 
 
