@@ -276,6 +276,22 @@ def test_chacha8_rows_rejection_shifts_later_draws(backend, oracle, count):
     assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 0x19664BCA, 2, count // 2 + 1, count // 2 + 5)).all()
 
 
+@pytest.mark.parametrize("rows,count", [(2, 8192), (3, 33280), (97, 8704), (1, 40000)])
+def test_chacha8_long_rows_one_workgroup_each(backend, oracle, rows, count):
+    """Few long rows are filled by 16 waves each, 1024 blocks per round; on
+    the reference KAT stream row 0 rejects its 6th raw draw, which shifts
+    every later place across all waves and rounds."""
+    d = backend.chacha8_prover_secret_fp_rows_device(KAT_SEED, 0x19664BCA, rows, count)
+    got = backend.download_device(d).reshape(rows, count)
+    backend.free_device(d)
+    assert (got == oracle.fp_rows(KAT_SEED, 0x19664BCA, rows, count)).all()
+    d2 = backend.chacha8_prover_secret_fp2_rows_padded_device(KAT_SEED, 0x19664BCA, rows, count // 2 + 1,
+                                                              count // 2 + 3)
+    got2 = backend.download_device(d2).view(np.uint64).reshape(rows, count // 2 + 3, 2)
+    backend.free_device(d2)
+    assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 0x19664BCA, rows, count // 2 + 1, count // 2 + 3)).all()
+
+
 def test_chacha8_rows_large(backend, oracle):
     seed = bytes(range(32))
     d = backend.chacha8_prover_secret_fp_rows_device(seed, 1000, 513, 512)

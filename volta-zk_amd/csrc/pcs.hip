@@ -698,25 +698,90 @@ __global__ __launch_bounds__(64 * CHACHA_WAVES) void chacha8_rows_kernel(chacha8
     }
 }
 
-int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
-                    uint64_t* out) {
+// Few long rows (an opening's mask rows: claims + 1 rows of tens of
+// thousands of draws) would leave most of the GPU idle with one wave per row
+// and serialise a hundred rounds.  Here a workgroup of CHACHA_WIDE waves fills
+// one row: a round takes 64 CHACHA_WIDE consecutive blocks (wave w, lane t:
+// block k0 + 64 w + t), each wave scans its lanes' kept counts, and the waves'
+// totals (in LDS) place each wave's run after those of the waves before it --
+// the same places as the one-wave kernel, in 1/CHACHA_WIDE of the rounds.
+constexpr int CHACHA_WIDE = 16;
+
+__global__ __launch_bounds__(64 * CHACHA_WIDE) void chacha8_rows_wide_kernel(chacha8::Key key, uint64_t base_domain,
+                                                                             size_t rows, size_t draws, size_t stride,
+                                                                             size_t zero_from, uint64_t* out) {
+    __shared__ int wave_total[CHACHA_WIDE];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (size_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        uint64_t* o = out + r * stride;
+        size_t done = 0;  // kept draws so far (uniform over the workgroup)
+        for (uint64_t k0 = 0; done < draws; k0 += 64 * CHACHA_WIDE) {
+            uint32_t w[16];
+            chacha8::block(key, base_domain + r, k0 + static_cast<uint64_t>(64 * wave + lane), w);
+            uint64_t v[8];
+            int kept = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                v[i] = static_cast<uint64_t>(w[2 * i]) | (static_cast<uint64_t>(w[2 * i + 1]) << 32);
+                kept += v[i] < chacha8::P ? 1 : 0;
+            }
+            int incl = kept;  // inclusive scan over the wave's lanes
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int y = __shfl_up(incl, d);
+                if (lane >= d) incl += y;
+            }
+            if (lane == 63) wave_total[wave] = incl;
+            __syncthreads();
+            int before = 0, total = 0;
+#pragma unroll
+            for (int q = 0; q < CHACHA_WIDE; ++q) {
+                const int t = wave_total[q];
+                before += q < wave ? t : 0;
+                total += t;
+            }
+            size_t m = done + static_cast<size_t>(before + incl - kept);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (v[i] < chacha8::P) {
+                    if (m < draws) o[m] = v[i];
+                    ++m;
+                }
+            }
+            done += static_cast<size_t>(total);
+            __syncthreads();  // wave_total is rewritten by the next round
+        }
+        for (size_t z = zero_from + threadIdx.x; z < stride; z += 64 * CHACHA_WIDE) o[z] = 0;
+    }
+}
+
+// Rows of `draws` kept values at `stride` words, zero from zero_from: one wave
+// per row, or a workgroup per row for few long rows.
+static int chacha8_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t draws,
+                        size_t stride, size_t zero_from, uint64_t* out) {
     const chacha8::Key key = chacha8::key_from_seed(seed);
-    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, CHACHA_WAVES, size_t{1} << 20)),
-                       dim3(64 * CHACHA_WAVES), 0, c->stream, key, base_domain, rows, count, count, count, out);
+    if (rows <= 1024 && draws >= 8192)
+        hipLaunchKernelGGL(chacha8_rows_wide_kernel, dim3(static_cast<unsigned>(rows)), dim3(64 * CHACHA_WIDE), 0,
+                           c->stream, key, base_domain, rows, draws, stride, zero_from, out);
+    else
+        hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, CHACHA_WAVES, size_t{1} << 20)),
+                           dim3(64 * CHACHA_WAVES), 0, c->stream, key, base_domain, rows, draws, stride, zero_from,
+                           out);
     VMX_HIP(c, hipGetLastError());
     return 0;
+}
+
+int chacha8_fp_rows(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
+                    uint64_t* out) {
+    return chacha8_rows(c, seed, base_domain, rows, count, count, count, out);
 }
 
 // Fp2 rows: element j of a row is (draw 2j, draw 2j + 1); elements count ..
 // padded - 1 are zero.
 int chacha8_fp2_rows_padded(Context* c, const uint8_t seed[32], uint64_t base_domain, size_t rows, size_t count,
                             size_t padded, Fp2* out) {
-    const chacha8::Key key = chacha8::key_from_seed(seed);
-    hipLaunchKernelGGL(chacha8_rows_kernel, dim3(grid_for(rows, CHACHA_WAVES, size_t{1} << 20)),
-                       dim3(64 * CHACHA_WAVES), 0, c->stream, key, base_domain, rows, 2 * count, 2 * padded,
-                       2 * count, reinterpret_cast<uint64_t*>(out));
-    VMX_HIP(c, hipGetLastError());
-    return 0;
+    return chacha8_rows(c, seed, base_domain, rows, 2 * count, 2 * padded, 2 * count,
+                        reinterpret_cast<uint64_t*>(out));
 }
 
 // ---- measurement probes ---------------------------------------------------------------------------
