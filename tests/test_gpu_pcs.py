@@ -371,6 +371,36 @@ def test_stats_contract_of_a_cold_encode():
         assert ws + res + cached == live and res == 0
 
 
+def test_deferred_timing_records_the_events_it_reads():
+    """Deferred events (policy 0): a device-only primitive records its two
+    kernel markers and nothing else, so each call costs two event records and,
+    at the flush, one elapsed-time query; a host-pointer primitive also times
+    its upload and download (h2d_ns, d2h_ns)."""
+    from volta_mi355x import FP2, Backend
+    with Backend(timing_policy=0) as b:
+        a, t = b.alloc_device(64, FP2), b.alloc_device(64, FP2)
+        b.zero_device(a, 0, 64)
+        b.zero_device(t, 0, 64)
+        L, r = b.lib, b.raw
+        for _ in range(600):  # every ring slot has its events created
+            assert L.volta_cuda_fp2_add_inplace_device(r, t.id, 0, a.id, 0, 64) == 0
+        s0 = b.get_stats()
+        for _ in range(100):
+            assert L.volta_cuda_fp2_add_inplace_device(r, t.id, 0, a.id, 0, 64) == 0
+        s1 = b.get_stats()
+        assert s1["timing_event_api_calls"] - s0["timing_event_api_calls"] == 100 * 3
+        assert s1["timing_records"] - s0["timing_records"] == 100
+        assert s1["h2d_ns"] == s0["h2d_ns"] and s1["d2h_ns"] == s0["d2h_ns"]
+        msgs = rand_fp(5, (4, 300))
+        got = b.ntt_fp_batch(msgs, 4, 300, 1 << 10)
+        s2 = b.get_stats()
+        assert s2["h2d_ns"] > s1["h2d_ns"] and s2["d2h_ns"] > s1["d2h_ns"]
+        assert s2["kernel_ns"]["pcs_ntt"] > s1["kernel_ns"]["pcs_ntt"]
+        for x in (a, t):
+            b.free_device(x)
+    assert got.shape == (4, 1 << 10)
+
+
 def test_coarse_timing_scope_and_wall_only_policy():
     import ctypes
     from volta_mi355x import Backend

@@ -151,7 +151,7 @@ int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size
     uint64_t h2d = 0;
     TwiddleSet* t = nullptr;
     if (ensure_twiddles(c, n, &h2d, &t)) return -1;
-    if (begin_op(c)) return -1;
+    if (begin_op_h2d(c)) return -1;
     // Compact rows cross PCIe once; zero padding happens in the kernel load.
     if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<uint64_t>(c, WS_IN), msgs, in_bytes, hipMemcpyHostToDevice, c->stream));
     h2d += in_bytes;
@@ -189,7 +189,7 @@ VMX_API int volta_cuda_ntt_fp2(void* raw, const Fp2* msg, size_t msg_len, size_t
         uint64_t h2d = 0;
         TwiddleSet* t = nullptr;
         if (ensure_twiddles(c, n, &h2d, &t)) return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), msg, in_bytes, hipMemcpyHostToDevice, c->stream));
         if (bytes > in_bytes && zero_bytes(c, ws<unsigned char>(c, WS_IN) + in_bytes, bytes - in_bytes)) return -1;
         h2d += bytes;
@@ -315,7 +315,7 @@ VMX_API int volta_cuda_pcs_combine_rows(void* raw, const int16_t* weights, const
         if (ensure_ws(c, WS_IN, wb) || ensure_ws(c, WS_AUX0, std::max<size_t>(pb, 8)) || ensure_ws(c, WS_AUX1, cb) ||
             ensure_ws(c, WS_OUT, ob))
             return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), weights, wb, hipMemcpyHostToDevice, c->stream));
         if (pb) VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), pads, pb, hipMemcpyHostToDevice, c->stream));
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX1), coeffs, cb, hipMemcpyHostToDevice, c->stream));
@@ -400,7 +400,7 @@ VMX_API int volta_cuda_pcs_gather_columns(void* raw, const uint64_t* matrix, siz
             return fail_msg(c, "PCS column-gather geometry overflows size_t");
         const size_t ib = queries * 4;
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_AUX0, ib) || ensure_ws(c, WS_OUT, ob)) return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), idx, ib, hipMemcpyHostToDevice, c->stream));
         if (mark_op(c, 1)) return -1;
@@ -741,7 +741,7 @@ VMX_API int volta_cuda_hash_fp_columns(void* raw, const uint64_t* matrix, size_t
             return fail_msg(c, "PCS hash matrix geometry overflows size_t");
         const size_t hb = cols * 32;
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_OUT, hb)) return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
         if (mark_op(c, 1)) return -1;
         if (merkle_column_leaves(c, ws<uint64_t>(c, WS_IN), rows, cols, false, ws<uint32_t>(c, WS_OUT))) return -1;
@@ -853,7 +853,7 @@ VMX_API int volta_cuda_x4b_ntt_fp2(void* raw, const Fp2* coefficients, size_t co
         uint64_t h2d = 0;
         X4Tables tb;
         if (x4_tables(c, log2_of(n), &h2d, &tb)) return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), coefficients, in_bytes, hipMemcpyHostToDevice, c->stream));
         h2d += in_bytes;
         if (mark_op(c, 1)) return -1;
@@ -992,7 +992,7 @@ VMX_API int volta_cuda_x4c_direct_fold_pinned_tile(void* raw, uint64_t pinned_id
         uint64_t h2d = 0;
         X4Tables tb;
         if (x4_tables(c, log2_of(input_len), &h2d, &tb)) return -1;
-        if (begin_op(c)) return -1;
+        if (begin_op_h2d(c)) return -1;
         const auto t0 = std::chrono::steady_clock::now();
         const hipError_t e = hipMemcpyAsync(scratch, src, tile_bytes, hipMemcpyHostToDevice, c->stream);
         const auto t1 = std::chrono::steady_clock::now();

@@ -406,12 +406,13 @@ int begin_op(Context* c) {
             c->counter_active = true;
             return 0;
         case TIMING_EVENTS_DEFERRED: {
+            // The record's opening event is only needed to time a host upload
+            // before marker 1 (begin_op_h2d); a device-only primitive records
+            // markers 1 and 2 alone, two event records per call instead of four.
             size_t slot = 0;
             if (ring_take(c, &slot)) return -1;
             c->active_slot = slot;
             c->record_active = true;
-            VMX_HIP(c, ev_record(c, c->ring[slot].ev[0]));
-            c->ring[slot].mask |= 1;
             return 0;
         }
         case TIMING_EVENTS:
@@ -423,6 +424,15 @@ int begin_op(Context* c) {
             c->phase_start = std::chrono::steady_clock::now();
             return 0;
     }
+}
+
+int begin_op_h2d(Context* c) {
+    if (begin_op(c)) return -1;
+    if (c->timing_mode == TIMING_EVENTS_DEFERRED && !c->coarse_active) {
+        VMX_HIP(c, ev_record(c, c->ring[c->active_slot].ev[0]));
+        c->ring[c->active_slot].mask |= 1;
+    }
+    return 0;
 }
 
 int mark_op(Context* c, int which) {
@@ -488,10 +498,15 @@ int finish_op(Context* c, int op, uint64_t h2d, uint64_t d2h, uint64_t d2d, uint
         case TIMING_EVENTS_DEFERRED: {
             if (!c->record_active) return fail_msg(c, "deferred finish without record");
             TimingRecord& r = c->ring[c->active_slot];
-            VMX_HIP(c, ev_record(c, r.ev[3]));
-            r.mask |= 8;
+            if (d2h) {  // the closing event only times a download after marker 2
+                VMX_HIP(c, ev_record(c, r.ev[3]));
+                r.mask |= 8;
+            }
             r.op = op;
-            r.h2d = h2d;
+            // upload time is measured when the primitive opened with
+            // begin_op_h2d (twiddle tables uploaded before the record count
+            // their bytes only)
+            r.h2d = (r.mask & 1) ? h2d : 0;
             r.d2h = d2h;
             ring_commit(c);
             account(c, op, h2d, d2h, d2d, zeroed, generated);

@@ -324,6 +324,8 @@ int ensure_grid_twiddles(Context* c, TwiddleSet* t, size_t bytes, int (*build)(C
 
 // ---- timing/accounting (one primitive = begin, [mark1], [mark2], finish) ---------
 int begin_op(Context* c);
+// begin_op for a primitive that uploads host data before marker 1: its upload is timed.
+int begin_op_h2d(Context* c);
 int mark_op(Context* c, int which);
 int finish_op(Context* c, int op, uint64_t h2d, uint64_t d2h, uint64_t d2d = 0,
               uint64_t zeroed = 0, uint64_t generated = 0);
