@@ -244,37 +244,52 @@ __global__ __launch_bounds__(COMB_THREADS) void combine_i16_partial(const int16_
 }
 
 // Pad columns j in [cols, cols+pad): full field products.
-constexpr int PAD_UNROLL = 8;
+constexpr int PAD_UNROLL = 8;  // rows whose loads are in flight together
+constexpr int PAD_WAVES = 4;   // the chunk's rows split four ways, summed in LDS
 
-__global__ void combine_pads_partial(const uint64_t* pads, const Fp2* coeffs, const uint32_t* nz, Fp2* partials,
-                                     size_t rows, size_t cols, size_t pad, size_t msg_len, size_t combinations,
-                                     size_t chunk, int direct) {
-    const size_t p = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const size_t comb = blockIdx.z;
-    if (p >= pad) return;
-    const size_t ck = blockIdx.y;
-    if (!nz[ck * combinations + comb]) {  // zero coefficients: as combine_i16_partial
-        if (direct) partials[(ck * combinations + comb) * msg_len + cols + p] = Fp2{0, 0};
+// A workgroup takes 64 pad columns (one per lane) of one (chunk, combination);
+// its four waves sum a quarter of the chunk's rows each.  An opening's
+// proximity pass has a single combination: one thread per column and chunk
+// would leave most CUs idle and serialise the chunk's row loads.
+__global__ __launch_bounds__(64 * PAD_WAVES) void combine_pads_partial(const uint64_t* pads, const Fp2* coeffs,
+                                                                      const uint32_t* nz, Fp2* partials, size_t rows,
+                                                                      size_t cols, size_t pad, size_t msg_len,
+                                                                      size_t combinations, size_t chunk, int direct) {
+    __shared__ Fp2 red[PAD_WAVES - 1][64];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const size_t p = static_cast<size_t>(blockIdx.x) * 64 + lane;
+    const size_t comb = blockIdx.z, ck = blockIdx.y;
+    Fp2* dst = partials + (ck * combinations + comb) * msg_len + cols + p;
+    if (!nz[ck * combinations + comb]) {  // zero coefficients (uniform): as combine_i16_partial
+        if (direct && wave == 0 && p < pad) *dst = Fp2{0, 0};
         return;
     }
-    const size_t r0 = ck * chunk, r1 = min(rows, r0 + chunk);
+    const size_t c0 = ck * chunk, c1 = min(rows, c0 + chunk);
+    const size_t per = (c1 - c0 + PAD_WAVES - 1) / PAD_WAVES;
+    const size_t r0 = min(c1, c0 + wave * per), r1 = min(c1, r0 + per);
+    const size_t pc = p < pad ? p : pad - 1;  // in bounds; the column is masked at the write
     const Fp2* cf = coeffs + comb * rows;
     Fp2 acc{0, 0};
     size_t i = r0;
-    // PAD_UNROLL rows' coefficient and pad loads in flight before their products
     for (; i + PAD_UNROLL <= r1; i += PAD_UNROLL) {
         Fp2 cv[PAD_UNROLL];
         uint64_t pv[PAD_UNROLL];
 #pragma unroll
         for (int u = 0; u < PAD_UNROLL; ++u) {
             cv[u] = cf[i + u];
-            pv[u] = pads[(i + u) * pad + p];
+            pv[u] = pads[(i + u) * pad + pc];
         }
 #pragma unroll
         for (int u = 0; u < PAD_UNROLL; ++u) acc = gl::fp2_add(acc, gl::fp2_mul_base(cv[u], pv[u]));
     }
-    for (; i < r1; ++i) acc = gl::fp2_add(acc, gl::fp2_mul_base(cf[i], pads[i * pad + p]));
-    partials[(ck * combinations + comb) * msg_len + cols + p] = acc;
+    for (; i < r1; ++i) acc = gl::fp2_add(acc, gl::fp2_mul_base(cf[i], pads[i * pad + pc]));
+    if (wave > 0) red[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && p < pad) {
+#pragma unroll
+        for (int o = 0; o < PAD_WAVES - 1; ++o) acc = gl::fp2_add(acc, red[o][lane]);
+        *dst = acc;
+    }
 }
 
 // Dense u64 rows: 128-bit products accumulated in three 64-bit limbs, folded
@@ -437,9 +452,9 @@ static int combine_launch(Context* c, const int16_t* w, const uint64_t* pads, co
         VMX_HIP(c, hipGetLastError());
     }
     if (pad) {
-        const dim3 g(static_cast<unsigned>((pad + 255) / 256), static_cast<unsigned>(chunks),
+        const dim3 g(static_cast<unsigned>((pad + 63) / 64), static_cast<unsigned>(chunks),
                      static_cast<unsigned>(combinations));
-        hipLaunchKernelGGL(combine_pads_partial, g, dim3(256), 0, c->stream, pads, coeffs,
+        hipLaunchKernelGGL(combine_pads_partial, g, dim3(64 * PAD_WAVES), 0, c->stream, pads, coeffs,
                            static_cast<const uint32_t*>(nz), part, rows, cols, pad, msg_len, combinations, chunk,
                            direct);
         VMX_HIP(c, hipGetLastError());
