@@ -918,7 +918,8 @@ __global__ __launch_bounds__(256) void eq_rows_kernel(const Fp2* __restrict__ po
     }
 }
 
-constexpr int DOT_THREADS = 256;
+constexpr int DOT_THREADS = 1024;  // 16 waves per row: a claim's mask row is 2^13..2^17 long
+constexpr int DOT_UNROLL = 4;      // products whose loads are in flight together
 
 __device__ __forceinline__ Fp2 fp2_shfl_xor(Fp2 x, int m) {
     const uint64_t c0 = __shfl_xor(x.c0, m), c1 = __shfl_xor(x.c1, m);
@@ -935,8 +936,20 @@ __global__ __launch_bounds__(DOT_THREADS) void fp2_row_dots_kernel(const Fp2* __
     const int t = threadIdx.x;
     for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
         Fp2 acc{0, 0};
-        for (size_t j = t; j < len; j += DOT_THREADS)
-            acc = gl::fp2_add(acc, gl::fp2_mul(a[row * a_stride + j], b[row * b_stride + j]));
+        const Fp2* ar = a + row * a_stride;
+        const Fp2* br = b + row * b_stride;
+        size_t j = t;
+        for (; j + (DOT_UNROLL - 1) * DOT_THREADS < len; j += DOT_UNROLL * DOT_THREADS) {
+            Fp2 x[DOT_UNROLL], y[DOT_UNROLL];
+#pragma unroll
+            for (int u = 0; u < DOT_UNROLL; ++u) {
+                x[u] = ar[j + u * DOT_THREADS];
+                y[u] = br[j + u * DOT_THREADS];
+            }
+#pragma unroll
+            for (int u = 0; u < DOT_UNROLL; ++u) acc = gl::fp2_add(acc, gl::fp2_mul(x[u], y[u]));
+        }
+        for (; j < len; j += DOT_THREADS) acc = gl::fp2_add(acc, gl::fp2_mul(ar[j], br[j]));
 #pragma unroll
         for (int m = 32; m > 0; m >>= 1) acc = gl::fp2_add(acc, fp2_shfl_xor(acc, m));
         if ((t & 63) == 0) part[t >> 6] = acc;
