@@ -132,6 +132,8 @@ struct SrcU64 {
     }
     // Offset of the gather's rows against its tiles (see gather_reg).
     __device__ __forceinline__ uint32_t rotation() const { return reverse ? 1u : 0u; }
+    // A tile's u64 runs are whole lines: tiles go to the XCDs round-robin.
+    static constexpr bool SWIZZLE = false;
     __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t plane, int PL) const {
         const uint64_t ci = idx < len ? idx : 0;
         return Raw{x[(row * x_stride + ci) * PL + plane]};
@@ -158,6 +160,9 @@ struct SrcMsgI16 {
     __host__ __device__ uint64_t extent(uint64_t n) const { return cols + pad > n ? n : cols + pad; }
     __device__ __forceinline__ uint64_t index(uint64_t idx, uint64_t) const { return idx; }
     __device__ __forceinline__ uint32_t rotation() const { return 0u; }
+    // A tile's i16 runs are 32 bytes, a quarter of a line: consecutive tiles
+    // run on one XCD so that the line is fetched into its L2 once.
+    static constexpr bool SWIZZLE = true;
     __device__ __forceinline__ Raw fetch(uint64_t row, uint64_t idx, uint32_t, int) const {
         const uint64_t wi = idx < cols ? idx : 0;
         const uint64_t pi = idx >= cols && idx - cols < pad ? idx - cols : 0;
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(THREADS) void gather_reg(Src src, uint64_t* __restr
     __syncthreads();
     uint64_t nat0, row0;
     int mid_bits;
-    gather_tile(nb, RB, qb, d, nat0, row0, mid_bits);
+    gather_tile<Src::SWIZZLE>(nb, RB, qb, d, nat0, row0, mid_bits);
     const int sh = nb - RB;
     const uint64_t nmask = (uint64_t{1} << nb) - 1, lmask = (uint64_t{1} << sh) - 1;
     const uint32_t rot = sh > 0 ? src.rotation() : 0u;

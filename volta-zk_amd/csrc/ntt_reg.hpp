@@ -43,9 +43,10 @@ __host__ __device__ constexpr int pass_bits(int nb, int planes) { return planes 
 // Tile index of this workgroup.  Workgroups are dispatched round-robin over
 // the 8 XCDs (blockIdx.x mod 8); with XCD_SWIZZLE the tiles an XCD runs back to
 // back are consecutive, so neighbouring tiles' shared cache lines meet in one L2.
+template <bool SWIZZLE = XCD_SWIZZLE>
 __device__ __forceinline__ uint64_t tile_id() {
     const uint64_t b = blockIdx.x;
-    if constexpr (XCD_SWIZZLE) {
+    if constexpr (SWIZZLE) {
         const uint64_t g = gridDim.x;
         if ((g & 7) == 0) return (b & 7) * (g >> 3) + (b >> 3);
     }
@@ -108,11 +109,12 @@ struct Digits {
 // row's first input, its first row row0, and mid_bits, the width of the
 // middle digits (rows of one tile are 2^mid_bits apart).  Tiles run over the
 // groups of 2^qb first digits fastest.
+template <bool SWIZZLE = XCD_SWIZZLE>
 __device__ __forceinline__ void gather_tile(int nb, int rb, int qb, const Digits& d, uint64_t& nat0, uint64_t& row0,
                                             int& mid_bits) {
     mid_bits = nb - rb - d.r1;
     const int gbits = d.r1 - qb;
-    const uint64_t blk = tile_id();
+    const uint64_t blk = tile_id<SWIZZLE>();
     const uint64_t g = blk & ((uint64_t{1} << gbits) - 1);
     const uint64_t rest = blk >> gbits;
     uint64_t natr = 0;
