@@ -302,6 +302,29 @@ def test_chacha8_rows_large(backend, oracle):
 
 # ---- seam contract: errors and stats -------------------------------------------------
 
+def test_host_geometry_whose_byte_counts_overflow(backend):
+    """Host-pointer calls whose element counts multiply past 2^64 are refused
+    before any staging copy or launch (each factor of a byte count is checked,
+    not only the last multiplication)."""
+    lib, raw = backend.lib, backend.raw
+    w = np.zeros(8, np.int16)
+    m = np.zeros(8, np.uint64)
+    co = np.zeros(4, np.uint64)
+    idx = np.zeros(1, np.uint32)
+    out = np.zeros(64, np.uint64)
+    big = 1 << 62
+    assert lib.volta_cuda_pcs_combine_rows(raw, w.ctypes.data, None, co.ctypes.data, big, 8, 0, 1,
+                                           out.ctypes.data) != 0
+    assert "overflows size_t" in backend.last_error()
+    assert lib.volta_cuda_pcs_combine_rows(raw, w.ctypes.data, m.ctypes.data, co.ctypes.data, 4, 2, big, 1,
+                                           out.ctypes.data) != 0
+    assert "overflows size_t" in backend.last_error()
+    assert lib.volta_cuda_pcs_gather_columns(raw, m.ctypes.data, big, 8, idx.ctypes.data, 1, out.ctypes.data) != 0
+    assert "overflows size_t" in backend.last_error()
+    assert lib.volta_cuda_hash_fp_columns(raw, m.ctypes.data, big, 16, out.ctypes.data) != 0
+    assert "overflows size_t" in backend.last_error()
+
+
 def test_geometry_and_id_errors(backend):
     from volta_mi355x import GpuError, InvalidInput
     buf = backend.alloc_device(16, np.uint64)

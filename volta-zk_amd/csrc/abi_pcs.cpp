@@ -145,7 +145,7 @@ VMX_API int volta_cuda_ntt_fp2_batch_device(void* raw, uint64_t in_id, size_t in
 namespace {
 int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size_t n, uint64_t* out) {
     size_t total = 0, bytes = 0, in_bytes = 0;
-    if (!mul_ok(rows, n, &total) || !mul_ok(total, 8, &bytes) || !mul_ok(rows * msg_len, 8, &in_bytes))
+    if (!mul_ok(rows, n, &total) || !mul_ok(total, 8, &bytes) || !mul3_ok(rows, msg_len, 8, &in_bytes))
         return fail_msg(c, "Fp NTT geometry overflows size_t");
     if (ensure_ws(c, WS_IN, std::max<size_t>(in_bytes, 8)) || ensure_ws(c, WS_OUT, bytes)) return -1;
     uint64_t h2d = 0;
@@ -309,8 +309,8 @@ VMX_API int volta_cuda_pcs_combine_rows(void* raw, const int16_t* weights, const
         return fail_msg(c, "invalid PCS row-combination geometry");
     return guarded(c, "PCS row combination", [&] {
         size_t wb = 0, pb = 0, cb = 0, ob = 0;
-        if (!mul_ok(rows * cols, 2, &wb) || !mul_ok(rows * pad, 8, &pb) || !mul_ok(combinations * rows, 16, &cb) ||
-            !mul_ok(combinations * (cols + pad), 16, &ob))
+        if (!mul3_ok(rows, cols, 2, &wb) || !mul3_ok(rows, pad, 8, &pb) || !mul3_ok(combinations, rows, 16, &cb) ||
+            cols + pad < cols || !mul3_ok(combinations, cols + pad, 16, &ob))
             return fail_msg(c, "PCS row-combination geometry overflows size_t");
         if (ensure_ws(c, WS_IN, wb) || ensure_ws(c, WS_AUX0, std::max<size_t>(pb, 8)) || ensure_ws(c, WS_AUX1, cb) ||
             ensure_ws(c, WS_OUT, ob))
@@ -396,7 +396,7 @@ VMX_API int volta_cuda_pcs_gather_columns(void* raw, const uint64_t* matrix, siz
         if (idx[q] >= cols) return fail_msg(c, "PCS column-gather index out of range");
     return guarded(c, "PCS column gather", [&] {
         size_t mb = 0, ob = 0;
-        if (!mul_ok(rows * cols, 8, &mb) || !mul_ok(rows * queries, 8, &ob))
+        if (!mul3_ok(rows, cols, 8, &mb) || !mul3_ok(rows, queries, 8, &ob))
             return fail_msg(c, "PCS column-gather geometry overflows size_t");
         const size_t ib = queries * 4;
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_AUX0, ib) || ensure_ws(c, WS_OUT, ob)) return -1;
@@ -710,7 +710,7 @@ VMX_API int volta_cuda_merkle_paths_device(void* raw, uint64_t tree_id, size_t t
         size_t bits = 0;
         while ((size_t{1} << bits) < leaves) ++bits;
         size_t tb = 0, pb = 0;
-        if (!mul_ok(2 * leaves - 1, 32, &tb) || !mul_ok(queries * bits, 32, &pb))
+        if (leaves > SIZE_MAX / 2 || !mul_ok(2 * leaves - 1, 32, &tb) || !mul3_ok(queries, bits, 32, &pb))
             return fail_msg(c, "resident Merkle path geometry overflows size_t");
         void *tree = nullptr, *idx = nullptr, *paths = nullptr;
         if (region_elems(c, tree_id, tree_off_bytes, tb, 1, &tree, true) ||
@@ -736,10 +736,9 @@ VMX_API int volta_cuda_hash_fp_columns(void* raw, const uint64_t* matrix, size_t
     if (!c || !matrix || !leaves || rows < 8 || rows % 8 || !pow2_or_one(cols))
         return fail_msg(c, "invalid PCS hash matrix geometry");
     return guarded(c, "PCS column hashes", [&] {
-        size_t mb = 0;
-        if (!mul_ok(rows * cols, 8, &mb) || rows * cols / cols != rows)
+        size_t mb = 0, hb = 0;
+        if (!mul3_ok(rows, cols, 8, &mb) || !mul_ok(cols, 32, &hb))
             return fail_msg(c, "PCS hash matrix geometry overflows size_t");
-        const size_t hb = cols * 32;
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_OUT, hb)) return -1;
         if (begin_op_h2d(c)) return -1;
         VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));

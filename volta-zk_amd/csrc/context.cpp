@@ -73,6 +73,11 @@ bool mul_ok(size_t a, size_t b, size_t* out) {
     return true;
 }
 
+bool mul3_ok(size_t a, size_t b, size_t c, size_t* out) {
+    size_t ab = 0;
+    return mul_ok(a, b, &ab) && mul_ok(ab, c, out);
+}
+
 bool add_ok(size_t a, size_t b, size_t* out) {
     if (b > std::numeric_limits<size_t>::max() - a) return false;
     *out = a + b;

@@ -278,6 +278,8 @@ int reject(Context* c, const char* msg) noexcept;
 
 // ---- geometry helpers -----------------------------------------------------------
 bool mul_ok(size_t a, size_t b, size_t* out);
+// a * b * c without overflow (every partial product checked).
+bool mul3_ok(size_t a, size_t b, size_t c, size_t* out);
 bool add_ok(size_t a, size_t b, size_t* out);
 Resident* find_resident(Context* c, uint64_t id);
 // Resolve a byte region of a resident buffer; fails if out of bounds.
