@@ -7,22 +7,23 @@
 //
 // Four-step split n = 128 x 64, input index i = 64*i1 + i2 (i1 < 128, and
 // only i1 < 32 is non-zero), output index j = j1 + 128*j2:
-//   phase A (thread = coset s in 0..3 x column i2 in 0..63, s = wave):
-//       X[4 t1 + s] = sum_{i1<32} (x[64 i1 + i2] * w128^(s i1)) * w32^(i1 t1)
-//     i.e. the 128-point DFT of a 32-long column as four 32-point DFTs of
-//     pre-twiddled inputs.  w128^k is a power of two (or a difference of two)
-//     times a 16-bit integer, w32 = 2^78: shifts only.  Then
-//       Y[j1][i2] = X[j1] * w_n^(i2 j1)      (the only 64x64 products)
+//   phase A (wave S = outputs j1 in [32 S, 32 S + 32), all 64 columns):
+//       X[j1][i2] = sum_{i1<32} x[64 i1 + i2] * w128^(i1 j1)
+//     as an exact int8 matrix product on the matrix cores (enc13_mfma.hpp:
+//     the inputs split into two signed bytes, the DFT matrix into balanced
+//     base-256 digits, eight position sums folded to one field element), then
+//       Y[j1][i2] = X[j1][i2] * w_n^(i2 j1)      (the only 64x64 products)
 //   phase B (thread = row j1 x parity h, h = 1 - (wave & 1)): the 64-point DFT over
 //     i2 (w64 = 2^39) as its first radix-2 DIF stage followed by one 32-point
-//     DFT per parity; X[2k + h] goes to out[j1 + 128 (2k + h)], so each store
-//     instruction writes 64 consecutive u64.
+//     DFT per parity (w32 = 2^78: shifts only); X[2k + h] goes to
+//     out[j1 + 128 (2k + h)], so each store instruction writes 64 consecutive u64.
 // A persistent grid of 4-wave workgroups walks the rows; Y lives in LDS with a
 // padded pitch.
 // HBM traffic per row: 4 KiB of i16 read + 64 KiB of u64 written.
 #include <hip/hip_runtime.h>
 
 #include "context.hpp"
+#include "enc13_mfma.hpp"
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
 #include "kernels.hpp"
@@ -39,22 +40,11 @@ constexpr int K = 32;      // non-zero i1 range (cols <= K * N2 = 2048)
 constexpr int PITCH = 65;  // u64 per LDS row of Y
 constexpr int THREADS = 256;
 constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
+constexpr size_t GRID_BYTES = size_t{N1} * N2 * sizeof(uint64_t);
+// The twiddle grid, then phase A's A fragments, then its accumulator init words.
+constexpr size_t TABLE_BYTES = GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int);
 
-// The 32 possibly non-zero entries x[64 i1 + i2] (i1 < 32) of one row, zero
-// past cols.  A raw buffer resource spanning exactly the row's cols entries
-// makes the hardware return 0 for the tail (an out-of-range buffer load reads
-// zero and touches no memory), and all 32 loads share one offset register.
-__device__ __forceinline__ void load_column(const int16_t* wr, size_t cols, int i2, uint32_t* x) {
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int16_t*>(wr), static_cast<short>(0), static_cast<int>(cols * sizeof(int16_t)), 0x00020000);
-    const int off = i2 * static_cast<int>(sizeof(int16_t));
-#pragma unroll
-    for (int q = 0; q < K / 2; ++q) {  // x[q] = w[2q] | w[2q + 1] << 16 (two i16 per register)
-        const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + 2 * q * N2 * static_cast<int>(sizeof(int16_t)), 0, 0);
-        const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + (2 * q + 1) * N2 * static_cast<int>(sizeof(int16_t)), 0, 0);
-        x[q] = (lo & 0xFFFFu) | (hi << 16);
-    }
-}
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 // Phase B's LDS half for row j1 and output parity H: reads Y's row and applies
 // the first radix-2 stage; the 32-point DFT over v then gives X[2k + H] in v[k].
@@ -69,79 +59,142 @@ __host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1
     });
 }
 
-// Coset S's pre-twiddled inputs in bit-reversed order: v[brev(i1)] = x[i1] w128^(S i1)
-// (xp: the column's 32 inputs, two i16 per word).
-template <int S>
-__device__ __forceinline__ void pretwiddle(const uint32_t* xp, uint64_t* v) {
-    gl::static_for<0, K>([&](auto ii) {
-        constexpr int i1 = decltype(ii)::value;
-        const int32_t xi = static_cast<int16_t>(static_cast<uint16_t>(i1 & 1 ? xp[i1 >> 1] >> 16 : xp[i1 >> 1]));
-        v[gl::bitrev_c(i1, 5)] = gl::i16_mul_w128<S * i1>(xi);
-    });
+// The row's inputs as the matrix product's B operand: lane l, column tile t
+// holds x[64 i1 + 16 t + (l & 15)] for i1 in [8 (l >> 4), 8 (l >> 4) + 8), two
+// per word as the digit pairs x ^ 0x80 (low byte (x & 255) - 128, high byte
+// x >> 8).  The raw buffer resource spans exactly the row's cols entries, so
+// the tail reads as 0 (an out-of-range buffer load reads zero and touches no
+// memory); all 32 loads share one offset register.
+__device__ __forceinline__ void load_frags(const int16_t* wr, size_t cols, int lane, v4i* xf) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int16_t*>(wr), static_cast<short>(0), static_cast<int>(cols * sizeof(int16_t)), 0x00020000);
+    const int off = static_cast<int>(sizeof(int16_t)) * (N2 * 8 * (lane >> 4) + (lane & 15));
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e0 = N2 * (2 * q) + 16 * t, e1 = N2 * (2 * q + 1) + 16 * t;
+            const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + 2 * e0, 0, 0);
+            const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off + 2 * e1, 0, 0);
+            xf[t][q] = static_cast<int>(((lo & 0xFFFFu) | (hi << 16)) ^ 0x00800080u);
+        }
 }
 
-// One wave's share of every row its workgroup owns: wave S runs phase A for
-// coset S and phase B for rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and
-// parity H = 1 - (S & 1).  S is uniform, so no lane diverges.  Only the
-// pre-twiddles and phase B's first stage depend on the wave; the DFTs and the
-// twiddle products are one copy of code for all four waves (43 KB of code
-// instead of 136 KB).  The even cosets (pure-shift pre-twiddles) take the
-// dearer parity 1 (sub + shift first stage), which evens out the waves' work
-// per row.  The workgroup walks rows blockIdx.x, blockIdx.x + gridDim.x, ...,
-// loading the next row's inputs while phase B of the current row runs.
+// One wave's share of every row its workgroup owns.  Wave S runs phase A for
+// the output pairs q in [8 S, 8 S + 8) (j1 = 4 q + 0..3) of all 64 columns:
+// its 16 A fragments (8 pairs x positions 0-3 and 4-7) stay in registers for
+// the kernel's life, and each row takes 64 products.  It then runs phase B for
+// rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and parity H = 1 - (S & 1).  S is
+// uniform, so no lane diverges.  The workgroup walks rows blockIdx.x,
+// blockIdx.x + gridDim.x, ..., loading the next row's inputs before phase B of
+// the current row.
 __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w, size_t cols, size_t rows,
-                                            const uint64_t* __restrict__ grid, uint64_t* __restrict__ out,
-                                            uint64_t* Y, int lane) {
+                                            const uint64_t* __restrict__ grid, const v4i* __restrict__ frags,
+                                            const v4i* __restrict__ init, uint64_t* __restrict__ out, uint64_t* Y,
+                                            int lane) {
+    constexpr int NP = enc13m::PAIRS;
     const int H = 1 - (S & 1);
-    const int j1 = (S >> 1) * 64 + lane;
-    uint32_t x[K / 2];
+    const int j1b = (S >> 1) * 64 + lane;
+    const int grp = lane >> 4, m = lane & 15;
+    const int q0 = NP * S;
+    v4i af[NP][2];
+#pragma unroll
+    for (int P = 0; P < NP; ++P)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) af[P][h] = frags[((q0 + P) * 2 + h) * 64 + lane];
+    // Buffer loads put the pair and tile parts of the twiddle and init addresses
+    // in the scalar offset, so no per-load address registers stay live.
+    const __amdgpu_buffer_rsrc_t grsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint64_t*>(grid), static_cast<short>(0), static_cast<int>(GRID_BYTES), 0x00020000);
+    const __amdgpu_buffer_rsrc_t irsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<v4i*>(init), static_cast<short>(0), static_cast<int>(enc13m::INIT_WORDS * sizeof(int)), 0x00020000);
+    const uint32_t g_off = static_cast<uint32_t>(((4 * q0 + grp) * N2 + m) * sizeof(uint64_t));
+    const uint32_t i_off = static_cast<uint32_t>((4 * q0 + grp) * 2 * sizeof(v4i));
+    auto g_load = [&](int P, int t) {  // w^(i2 j1) for j1 = 4 (q0 + P) + grp, i2 = 16 t + m
+        const uint32_t so = static_cast<uint32_t>((4 * P * N2 + 16 * t) * sizeof(uint64_t));
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(grsrc, g_off, so, 0);
+        return static_cast<uint64_t>(v[0]) | (static_cast<uint64_t>(v[1]) << 32);
+    };
+    auto c_load = [&](int P, int h) {  // init words of j1 = 4 (q0 + P) + grp, positions 4 h .. 4 h + 3
+        const uint32_t so = static_cast<uint32_t>((4 * P * 2 + h) * sizeof(v4i));
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(irsrc, i_off, so, 0);
+        return v4i{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]), static_cast<int>(v[3])};
+    };
+    v4i xf[4];
     size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
-    load_column(w + row * cols, cols, lane, x);
+    load_frags(w + row * cols, cols, lane, xf);
     for (; row < rows; row += gridDim.x) {
         // A SIMD holds one wave of each of two workgroups.  Phase A issues at a
         // higher wave priority than phase B, so when both waves are ready the
         // one heading for its workgroup's barrier goes first and the other fills
-        // its gaps (measured: 2.43 -> 2.27 ms on C3; priority 3 or 2/1 the same).
+        // its gaps (without the priorities the encode is about 10% slower).
         __builtin_amdgcn_s_setprio(1);
-        // Phase A: the four-step twiddles w_n^(i2 (4 t1 + S)) come from the
-        // L2-resident grid, loaded before the DFT so its arithmetic covers them.
-        uint64_t g[K];
+        // Software pipeline over the pairs: pair P + 1's products are issued
+        // before pair P's results are folded (the fold waits on the matrix
+        // cores otherwise), its init words two pairs ahead and its twiddles one
+        // pair ahead.
+        uint64_t g[NP][4];
+        v4i c[NP][2], d[NP][4][2];
+        c[0][0] = c_load(0, 0);
+        c[0][1] = c_load(0, 1);
+        c[1][0] = c_load(1, 0);
+        c[1][1] = c_load(1, 1);
 #pragma unroll
-        for (int t1 = 0; t1 < K; ++t1) g[t1] = grid[(4 * t1 + S) * N2 + lane];
-        __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the DFT
-        uint64_t v[K];
-        switch (S) {
-            case 0: pretwiddle<0>(x, v); break;
-            case 1: pretwiddle<1>(x, v); break;
-            case 2: pretwiddle<2>(x, v); break;
-            default: pretwiddle<3>(x, v); break;
+        for (int t = 0; t < 4; ++t) g[0][t] = g_load(0, t);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) d[0][t][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[0][h], xf[t], c[0][h], 0, 0, 0);
+#pragma unroll
+        for (int P = 0; P < NP; ++P) {
+            if (P + 2 < NP) {
+                c[P + 2][0] = c_load(P + 2, 0);
+                c[P + 2][1] = c_load(P + 2, 1);
+            }
+            if (P + 1 < NP) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) g[P + 1][t] = g_load(P + 1, t);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        d[P + 1][t][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[P + 1][h], xf[t], c[P + 1][h], 0, 0, 0);
+            }
+            const int j1 = 4 * (q0 + P) + grp;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int a[4] = {d[P][t][0][0], d[P][t][0][1], d[P][t][0][2], d[P][t][0][3]};
+                const int b[4] = {d[P][t][1][0], d[P][t][1][1], d[P][t][1][2], d[P][t][1][3]};
+                Y[j1 * PITCH + 16 * t + m] = gl::mul32x4(enc13m::recombine(a, b), g[P][t]);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // at most two pairs' products in registers
         }
-        gl::dit_pow2<5, gl::E_W32>(v);
-#pragma unroll
-        for (int t1 = 0; t1 < K; ++t1) Y[(4 * t1 + S) * PITCH + lane] = gl::mul32x4(v[t1], g[t1]);
         const size_t next = row + gridDim.x;
-        if (next < rows) load_column(w + next * cols, cols, lane, x);
+        if (next < rows) load_frags(w + next * cols, cols, lane, xf);
         __syncthreads();
         __builtin_amdgcn_s_setprio(0);
-        if (H == 0) phase_b_first<0>(Y, j1, v);
-        else phase_b_first<1>(Y, j1, v);
+        uint64_t v[K];
+        if (H == 0) phase_b_first<0>(Y, j1b, v);
+        else phase_b_first<1>(Y, j1b, v);
         // Y is rewritten by the next row's phase A.  Once every wave holds its
         // rows' first stage in registers the workgroup may move on, so the
         // DFTs and stores of phase B overlap the next phase A of faster waves.
         __syncthreads();
         gl::dit_pow2<5, gl::E_W32>(v);
-        uint64_t* o = out + row * N + j1 + N1 * H;
+        uint64_t* o = out + row * N + j1b + N1 * H;
 #pragma unroll
         for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);
     }
 }
 
 __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __restrict__ w, size_t cols, size_t rows,
-                                                          const uint64_t* __restrict__ grid,
+                                                          const uint64_t* __restrict__ tables,
                                                           uint64_t* __restrict__ out) {
     extern __shared__ uint64_t Y[];
     const int lane = threadIdx.x & 63;
-    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, grid, out, Y, lane);
+    const v4i* frags = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(tables) + GRID_BYTES);
+    const v4i* init = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(frags) + enc13m::FRAG_BYTES);
+    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane);
 }
 
 // grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
@@ -153,9 +206,22 @@ __global__ void build_grid13(const uint64_t* __restrict__ tw, uint64_t* __restri
     grid[idx] = e < N / 2 ? tw[e] : gl::neg(tw[e - N / 2]);
 }
 
+// Phase A's tables after the grid: the A fragments (enc13m::a_fragment, one
+// 16-byte fragment per thread) and the accumulator init words.
+__global__ void build_phase_a13(const uint64_t* __restrict__ tw, int8_t* __restrict__ frags, int* __restrict__ init) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < static_cast<int>(enc13m::FRAG_BYTES / 16)) enc13m::a_fragment(tw, idx, frags + 16 * idx);
+    if (idx < static_cast<int>(enc13m::INIT_WORDS)) init[idx] = enc13m::init_word(tw, idx >> 3, idx & 7);
+}
+
 int build_grid(Context* c, TwiddleSet* t) {
     hipLaunchKernelGGL(build_grid13, dim3((N1 * N2 + 255) / 256), dim3(256), 0, c->stream,
                        static_cast<const uint64_t*>(t->fwd), t->grid);
+    VMX_HIP(c, hipGetLastError());
+    int8_t* frags = reinterpret_cast<int8_t*>(t->grid) + GRID_BYTES;
+    int* init = reinterpret_cast<int*>(frags + enc13m::FRAG_BYTES);
+    hipLaunchKernelGGL(build_phase_a13, dim3(static_cast<unsigned>((enc13m::FRAG_BYTES / 16 + 255) / 256)), dim3(256),
+                       0, c->stream, static_cast<const uint64_t*>(t->fwd), frags, init);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
@@ -167,7 +233,7 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
     if (n != static_cast<size_t>(enc13::N) || cols == 0 || cols > static_cast<size_t>(enc13::K * enc13::N2))
         return 1;
     if (rows == 0) return 0;
-    if (ensure_grid_twiddles(c, t, size_t{enc13::N1} * enc13::N2 * sizeof(uint64_t), enc13::build_grid)) return -1;
+    if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return -1;
     // The LDS limit is an attribute of the kernel on the current device: set
     // it on every call (a host-side call of about a microsecond), so no flag
     // shared between contexts, threads or devices is needed.
