@@ -376,6 +376,32 @@ def test_pcs_encode_fused_and_chain_match_oracle(backend, oracle, rows, cols, pa
     assert (got_f == want).all()
 
 
+@pytest.mark.parametrize("cols", [1, 63, 64, 65, 1024, 2047, 2048])
+@pytest.mark.parametrize("kind", ["top band", "byte edges"])
+def test_fast_encode_byte_split_edges(backend, oracle, cols, kind):
+    """The n = 2^13 fast path splits each i16 into two signed bytes for the
+    matrix-core product (x = 256 (x >> 8) + ((x & 255) - 128) + 128): rows of
+    values whose high byte is 127 with a low byte >= 128 (32640 .. 32767), and
+    of every low-byte and high-byte extreme, at zero-tail lengths around the
+    64-column rows of the four-step split; every element against the oracle,
+    through the reference's two calls."""
+    rows, n = 33, 8192
+    g = np.random.Generator(np.random.PCG64(cols * 7 + len(kind)))
+    if kind == "top band":
+        w = g.integers(32640, 32768, size=rows * cols).astype(np.int16)
+    else:
+        edges = np.array([-32768, -32767, -32641, -32640, -129, -128, -127, -1, 0, 1, 127, 128, 255, 256, 32639,
+                          32640, 32767], np.int16)
+        w = g.choice(edges, size=rows * cols)
+    dw, dp = backend.upload_device(w), backend.alloc_device(1, np.uint64)
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, 0, n)
+    enc = backend.ntt_fp_batch_device(msgs, rows, n)  # the recorded rows: the fast path from the weights
+    got = backend.download_device(enc).reshape(rows, n)
+    for b in (dw, dp, msgs, enc):
+        backend.free_device(b)
+    assert (got == oracle.pcs_encode_i16(w, None, rows, cols, 0, n)).all()
+
+
 # ---- benchmark configurations ---------------------------------------------------------
 
 def test_c1_full_config(backend, oracle):
