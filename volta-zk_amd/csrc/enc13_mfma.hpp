@@ -91,18 +91,25 @@ __host__ __device__ inline int init_word(const uint64_t* tw_half, int j1, int po
 // representative, not necessarily below p (gl::mul32x4 takes any u64).
 // Adjacent positions pair into 32-bit sums b < 2^30, so V = L + H 2^32 with
 // L = b0 + b1 2^16 and H = b2 + b3 2^16 below 2^47; then V = lo + hi 2^64 with
-// hi < 2^16, and 2^64 = 2^32 - 1 (mod p).
-__host__ __device__ __forceinline__ uint64_t recombine(const int* a /* pos 0..3 */, const int* b /* pos 4..7 */) {
+// hi < 2^16, and 2^64 = 2^32 - 1 (mod p).  14 VALU instructions on gfx950.
+// k16 = 2^16 and keps = 2^32 - 1 come in as run-time values (kernel
+// arguments): as constants the compiler turns the products into 64-bit shifts
+// and adds, 8 more instructions per fold than the multiply-adds.
+__host__ __device__ __forceinline__ uint64_t recombine(const int* a /* pos 0..3 */, const int* b /* pos 4..7 */,
+                                                       uint32_t k16 = 65536u, uint32_t keps = 0xFFFFFFFFu) {
     const uint32_t b0 = static_cast<uint32_t>(a[0]) + (static_cast<uint32_t>(a[1]) << 8);
     const uint32_t b1 = static_cast<uint32_t>(a[2]) + (static_cast<uint32_t>(a[3]) << 8);
     const uint32_t b2 = static_cast<uint32_t>(b[0]) + (static_cast<uint32_t>(b[1]) << 8);
     const uint32_t b3 = static_cast<uint32_t>(b[2]) + (static_cast<uint32_t>(b[3]) << 8);
-    const uint64_t L = static_cast<uint64_t>(b0) + (static_cast<uint64_t>(b1) << 16);
-    const uint64_t H = static_cast<uint64_t>(b2) + (static_cast<uint64_t>(b3) << 16);
-    const uint64_t lo = L + (H << 32);
-    const uint64_t hi = (H >> 32) + (lo < L ? 1u : 0u);
-    const uint64_t r = lo + hi * gl::EPS;
-    return r < lo ? r + gl::EPS : r;  // a carry out of 2^64 is worth eps; r + eps cannot carry again
+    const uint64_t L = static_cast<uint64_t>(b1) * k16 + b0;  // one 32 x 32 + 64 multiply-add each
+    const uint64_t H = static_cast<uint64_t>(b3) * k16 + b2;
+    // lo = L + (H mod 2^32) 2^32, hi = (H >> 32) + its carry: V = lo + hi 2^64
+    unsigned c;
+    const uint32_t lo_hi = __builtin_addc(static_cast<uint32_t>(L >> 32), static_cast<uint32_t>(H), 0u, &c);
+    const uint32_t hi = static_cast<uint32_t>(H >> 32) + c;
+    const uint64_t lo = (static_cast<uint64_t>(lo_hi) << 32) | static_cast<uint32_t>(L);
+    const uint64_t r = static_cast<uint64_t>(hi) * keps + lo;  // 2^64 = eps
+    return r < lo ? static_cast<uint64_t>(1u) * keps + r : r;  // a carry out of 2^64 is worth eps, once
 }
 
 }  // namespace enc13m

@@ -91,7 +91,7 @@ __device__ __forceinline__ void load_frags(const int16_t* wr, size_t cols, int l
 __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w, size_t cols, size_t rows,
                                             const uint64_t* __restrict__ grid, const v4i* __restrict__ frags,
                                             const v4i* __restrict__ init, uint64_t* __restrict__ out, uint64_t* Y,
-                                            int lane) {
+                                            int lane, uint32_t k16, uint32_t keps) {
     constexpr int NP = enc13m::PAIRS;
     const int H = 1 - (S & 1);
     const int j1b = (S >> 1) * 64 + lane;
@@ -165,7 +165,7 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
             for (int t = 0; t < 4; ++t) {
                 const int a[4] = {d[P][t][0][0], d[P][t][0][1], d[P][t][0][2], d[P][t][0][3]};
                 const int b[4] = {d[P][t][1][0], d[P][t][1][1], d[P][t][1][2], d[P][t][1][3]};
-                Y[j1 * PITCH + 16 * t + m] = gl::mul32x4(enc13m::recombine(a, b), g[P][t]);
+                Y[j1 * PITCH + 16 * t + m] = gl::mul32x4(enc13m::recombine(a, b, k16, keps), g[P][t]);
             }
             __builtin_amdgcn_sched_barrier(0);  // at most two pairs' products in registers
         }
@@ -189,12 +189,13 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
 
 __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __restrict__ w, size_t cols, size_t rows,
                                                           const uint64_t* __restrict__ tables,
-                                                          uint64_t* __restrict__ out) {
+                                                          uint64_t* __restrict__ out, uint32_t k16, uint32_t keps) {
     extern __shared__ uint64_t Y[];
     const int lane = threadIdx.x & 63;
     const v4i* frags = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(tables) + GRID_BYTES);
     const v4i* init = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(frags) + enc13m::FRAG_BYTES);
-    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane);
+    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane, k16,
+                keps);
 }
 
 // grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
@@ -245,7 +246,7 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
     const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
     const unsigned blocks = static_cast<unsigned>(std::min(rows, per_cu * cus));
     hipLaunchKernelGGL(enc13::encode13_i16, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream, w, cols,
-                       rows, static_cast<const uint64_t*>(t->grid), out);
+                       rows, static_cast<const uint64_t*>(t->grid), out, 65536u, 0xFFFFFFFFu);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
