@@ -120,6 +120,13 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(irsrc, i_off, so, 0);
         return v4i{static_cast<int>(v[0]), static_cast<int>(v[1]), static_cast<int>(v[2]), static_cast<int>(v[3])};
     };
+    // The first two pairs' init words and the first pair's twiddles do not
+    // depend on the row: held in registers, so a row's phase A starts without
+    // waiting on L2.
+    const v4i c00 = c_load(0, 0), c01 = c_load(0, 1), c10 = c_load(1, 0), c11 = c_load(1, 1);
+    uint64_t g0[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) g0[t] = g_load(0, t);
     v4i xf[4];
     size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
     load_frags(w + row * cols, cols, lane, xf);
@@ -135,12 +142,12 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
         // pair ahead.
         uint64_t g[NP][4];
         v4i c[NP][2], d[NP][4][2];
-        c[0][0] = c_load(0, 0);
-        c[0][1] = c_load(0, 1);
-        c[1][0] = c_load(1, 0);
-        c[1][1] = c_load(1, 1);
+        c[0][0] = c00;
+        c[0][1] = c01;
+        c[1][0] = c10;
+        c[1][1] = c11;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) g[0][t] = g_load(0, t);
+        for (int t = 0; t < 4; ++t) g[0][t] = g0[t];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
