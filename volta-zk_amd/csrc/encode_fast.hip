@@ -13,7 +13,7 @@
 //     the inputs split into two signed bytes, the DFT matrix into balanced
 //     base-256 digits, eight position sums folded to one field element), then
 //       Y[j1][i2] = X[j1][i2] * w_n^(i2 j1)      (the only 64x64 products)
-//   phase B (thread = row j1 x parity h, h = 1 - (wave & 1)): the 64-point DFT over
+//   phase B (thread = row j1 x parity h, h alternating per row): the 64-point DFT over
 //     i2 (w64 = 2^39) as its first radix-2 DIF stage followed by one 32-point
 //     DFT per parity (w32 = 2^78: shifts only); X[2k + h] goes to
 //     out[j1 + 128 (2k + h)], so each store instruction writes 64 consecutive u64.
@@ -84,8 +84,11 @@ __device__ __forceinline__ void load_frags(const int16_t* wr, size_t cols, int l
 // the output pairs q in [8 S, 8 S + 8) (j1 = 4 q + 0..3) of all 64 columns:
 // its 16 A fragments (8 pairs x positions 0-3 and 4-7) stay in registers for
 // the kernel's life, and each row takes 64 products.  It then runs phase B for
-// rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and parity H = 1 - (S & 1).  S is
-// uniform, so no lane diverges.  The workgroup walks rows blockIdx.x,
+// rows j1 in [64 (S >> 1), 64 (S >> 1) + 64) and parity H, 1 - (S & 1) on the
+// workgroup's first row and flipped on each row after it: parity 1's first
+// stage costs about three times parity 0's, and a fixed parity per wave would
+// give the same SIMDs the longer share on every row.  S and H are uniform, so
+// no lane diverges.  The workgroup walks rows blockIdx.x,
 // blockIdx.x + gridDim.x, ..., loading the next row's inputs before phase B of
 // the current row.
 __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w, size_t cols, size_t rows,
@@ -93,7 +96,7 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
                                             const v4i* __restrict__ init, uint64_t* __restrict__ out, uint64_t* Y,
                                             int lane, uint32_t k16, uint32_t keps) {
     constexpr int NP = enc13m::PAIRS;
-    const int H = 1 - (S & 1);
+    int H = 1 - (S & 1);
     const int j1b = (S >> 1) * 64 + lane;
     const int grp = lane >> 4, m = lane & 15;
     const int q0 = NP * S;
@@ -191,6 +194,7 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
         uint64_t* o = out + row * N + j1b + N1 * H;
 #pragma unroll
         for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);
+        H ^= 1;
     }
 }
 
