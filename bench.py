@@ -269,6 +269,100 @@ def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
     return out
 
 
+FNV_OFFSET = 0xCBF29CE484222325
+
+
+def published_shapes(b, reps: int = 10) -> dict:
+    """The two shapes on this path for which the reference publishes GPU
+    times (benchmarks/results/p7-gpu-pcs-arithmetic-2026-07-11-366ec4a.json,
+    A100), with the reference's own inputs and output checksums, timed with
+    the library's HIP events (not part of `value`):
+    - P4_LAYER NTT (cuda/p7_pcs_arithmetic.cu:201-263): 1024 rows x 2^15,
+      in[idx] = (idx 0x9E3779B9 + 17) mod p for column j < 16896, else 0,
+      through volta_cuda_ntt_fp_batch_device on the pre-padded rows; checksum
+      0xbe7b90425a4c7229 over all outputs;
+    - the two-combination (:265-320): 1024 x 16384 u64 rows w[i] = (i
+      0x85EBCA6B + 29) mod p, coefficient rows q[i] = (37i+11, 53i+5) and c[i]
+      = (71i+7, 97i+13); checksum cs(uq) ^ cs(uc) 0x9E3779B97F4A7C15 =
+      0x856f9a96d8e01901.
+    Each checksum is recomputed from the device output of this run and must
+    match, or the leg raises."""
+    import numpy as np
+    from volta_mi355x import FP2
+    P = np.uint64(0xFFFF_FFFF_0000_0001)
+    L, r = b.lib, b.raw
+    mask = (1 << 64) - 1
+
+    def fnv(a):
+        a = np.ascontiguousarray(a).view(np.uint64).reshape(-1)
+        return int(L.volta_mi355x_fnv64_host(a.ctypes.data, a.size, FNV_OFFSET))
+
+    def timed(op, call):
+        for _ in range(2):
+            b._check(call())
+        b.synchronize()
+        b.reset_stats()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            b._check(call())
+        b.synchronize()
+        wall = (time.perf_counter() - t0) / reps
+        s = b.get_stats()
+        return s["kernel_ns"][op] / max(s["calls"][op], 1) / 1e6, wall * 1e3
+
+    out = {"source": "benchmarks/results/p7-gpu-pcs-arithmetic-2026-07-11-366ec4a.json (A100-SXM4-80GB)",
+           "reps": reps}
+    rows, n, msg_len = 1024, 1 << 15, 16896
+    idx = np.arange(rows * n, dtype=np.uint64)
+    x = ((idx * np.uint64(0x9E3779B9) + np.uint64(17)) % P).reshape(rows, n)
+    x[:, msg_len:] = 0
+    din = b.upload_device(x.reshape(-1))
+    del x, idx
+    dout = b.alloc_device(rows * n, np.uint64)
+    ms, wall = timed("pcs_ntt", lambda: L.volta_cuda_ntt_fp_batch_device(r, din.id, 0, rows, n, dout.id, 0))
+    cs = fnv(b.download_device(dout))
+    for d in (din, dout):
+        b.free_device(d)
+    if cs != 0xBE7B90425A4C7229:
+        raise RuntimeError(f"P4_LAYER NTT checksum {cs:#018x} != 0xbe7b90425a4c7229")
+    io = 2 * rows * n * 8
+    out["p4_layer_ntt"] = {
+        "call": "volta_cuda_ntt_fp_batch_device", "rows": rows, "n": n, "msg_len": msg_len,
+        "ms": round(ms, 4), "wall_ms_per_call": round(wall, 4), "gelem_per_s": round(rows * n / ms / 1e6, 2),
+        "read_write_bytes": io, "achieved_gbs": round(io / ms / 1e6, 1),
+        "checksum": f"{cs:#018x}", "checksum_expected": "0xbe7b90425a4c7229",
+        "reference_a100_ms": 6.386, "reference_a100_gelem_per_s": 5.25, "speedup_vs_reference_a100": round(6.386 / ms, 1)}
+
+    rows, cols = 1024, 16384
+    i = np.arange(rows * cols, dtype=np.uint64)
+    w = (i * np.uint64(0x85EBCA6B) + np.uint64(29)) % P
+    del i
+    k = np.arange(rows, dtype=np.uint64)
+    q = np.stack([(k * np.uint64(37) + np.uint64(11)) % P, (k * np.uint64(53) + np.uint64(5)) % P], 1)
+    c = np.stack([(k * np.uint64(71) + np.uint64(7)) % P, (k * np.uint64(97) + np.uint64(13)) % P], 1)
+    dm = b.upload_device(w)
+    dc = b.alloc_device(2 * rows, FP2)
+    b.upload_into(dc, 0, np.concatenate([q, c]).reshape(-1))
+    du = b.alloc_device(2 * cols, FP2)
+    ms, wall = timed("pcs_rows", lambda: L.volta_mi355x_combine_rows_fp_device(r, dm.id, 0, rows, cols, dc.id, 0, 2,
+                                                                              du.id, 0))
+    u = b.download_device(du).view(np.uint64).reshape(2, cols, 2)
+    for d in (dm, dc, du):
+        b.free_device(d)
+    cs = fnv(u[0]) ^ ((fnv(u[1]) * 0x9E3779B97F4A7C15) & mask)
+    if cs != 0x856F9A96D8E01901:
+        raise RuntimeError(f"combination checksum {cs:#018x} != 0x856f9a96d8e01901")
+    rd = rows * cols * 8
+    out["two_combination"] = {
+        "call": "volta_mi355x_combine_rows_fp_device (u64 rows, 2 Fp2 coefficient rows)", "rows": rows,
+        "cols": cols, "ms": round(ms, 4), "wall_ms_per_call": round(wall, 4),
+        "g_weight_elem_per_s": round(rows * cols / ms / 1e6, 2), "read_bytes": rd,
+        "achieved_gbs": round(rd / ms / 1e6, 1), "checksum": f"{cs:#018x}",
+        "checksum_expected": "0x856f9a96d8e01901", "reference_a100_ms": 1.918,
+        "speedup_vs_reference_a100": round(1.918 / ms, 1)}
+    return out
+
+
 def fp2_chain_peak(b, log_n: int = 20, rounds: int = 256, reps: int = 10) -> dict:
     """Integer multiply peak from the reference's Fp2 chain kernel
     (cuda/p7_goldilocks_roofline.cu:79-89: x = x*b + (j+1, 2j+3), `rounds`
@@ -524,7 +618,7 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
             t_all.append(time.perf_counter() - t0)
         t = statistics.median(t_all)
         return {"value": round(2 * sample * n / t / 1e9, 4), "unit": "Gelem/s", "cores": threads,
-                "cpu_model": cpu_model(), "kind": "port",
+                "cores_counted": cpu_cores_note(threads), "cpu_model": cpu_model(), "kind": "port",
                 "sample": f"{sample} of {rows_all} rows of c5 (forward + inverse + the combination over those rows; "
                           f"elements counted both ways as the GPU's), mean of 2 runs without warm-up, {t:.3f} s"}
     else:
@@ -549,6 +643,7 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
         "value": round(sample * n / t / 1e9, 4),
         "unit": "Gelem/s",
         "cores": threads,
+        "cores_counted": cpu_cores_note(threads),
         "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{sample} of {rows_all} rows of {name} ({step} over those rows), median of 3 after 1 warmup, "
@@ -557,13 +652,36 @@ def cpu_baseline(name: str, wl: Workload) -> dict:
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, then vendor, family,
+    model and stepping (a virtualised host may report only a generic model
+    name), then the logical CPUs the kernel lists."""
+    fields, logical = {}, 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                logical += 1
+            elif key in ("model name", "vendor_id", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = val.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = fields.get("model name", "unknown")
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("vendor_id", "cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ids}; {logical} logical CPUs listed)" if ids else name
+
+
+def cpu_cores_note(threads: int) -> str:
+    """How `cores` was counted (cgroup quota first, as the reference's
+    scripts/p7_gpu_pcs_arithmetic.py:52-58, then the affinity mask)."""
+    import oracle
+    quota = oracle.cgroup_cpu_quota()
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        affinity = os.cpu_count() or 1
+    q = f"cgroup cpu.max quota {quota}" if quota else "no cgroup cpu.max quota"
+    return f"{threads} threads: {q}, affinity mask {affinity} CPUs, the smaller taken"
 
 
 def traffic_for(name: str):
@@ -589,6 +707,7 @@ def main() -> int:
     ap.add_argument("--no-x4", action="store_true")
     ap.add_argument("--no-seam-chain", action="store_true")
     ap.add_argument("--no-reference-commits", action="store_true")
+    ap.add_argument("--no-published-shapes", action="store_true")
     ap.add_argument("--x4-log-n", type=int, default=24)
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -632,6 +751,10 @@ def main() -> int:
     if not a.no_seam_chain:
         log("seam chain (messages + NTT through the reference's calls)")
         chain_leg = seam_chain(b, wl)
+    shapes = None
+    if not a.no_published_shapes:
+        log("the reference's published shapes (P4_LAYER NTT, 1024 x 16384 two-combination)")
+        shapes = published_shapes(b)
     wl_close = wl.close
     commits = None
     if not a.no_reference_commits:
@@ -669,6 +792,8 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
             "traffic": traffic_for(a.config),
+            "traffic_source": ("copied from profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE x 2 + WRITE_SIZE of "
+                               "the same kernel, taken in separate runs), not measured in this run"),
             "algorithmic_bytes": alg,
             "avg_launch_ms": round(enc_s * 1e3, 4),
             "launches_per_step": launches_per_step,
@@ -683,6 +808,7 @@ def main() -> int:
         "commit_tree": tree,
         "x4": x4,
         "reference_commits": commits,
+        "reference_published_shapes": shapes,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -362,13 +362,16 @@ int volta_mi355x_pcs_encode_device(void* ctx, uint64_t w_id, size_t w_off, uint6
                                    size_t out_off);
 
 /* volta_cuda_pcs_combine_rows_device without any allocation.  No counterpart
- * in the reference: it is for callers that cannot allocate (code under HIP
- * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
- * partial sums live in a fixed 16 MiB device array per GPU (held until the
- * process ends); a combination whose partials need more is refused with an
- * error (C3's two combinations need 8 MiB).  All calls on one GPU share the
- * array: calls that overlap in time on one GPU race.  Same arguments,
- * results and RawStats as volta_cuda_pcs_combine_rows_device. */
+ * in the reference: it is for callers that cannot allocate (tight serving
+ * loops, harnesses that forbid hipMalloc).  Its partial sums live in a fixed
+ * 16 MiB device array per GPU (held until the process ends); a combination
+ * whose partials need more is refused with an error (C3's two combinations
+ * need 8 MiB).  All contexts on one GPU share the array; the library orders
+ * their uses on the device with a per-device event, so back-to-back calls
+ * from different contexts do not race, and each call rewrites every scratch
+ * word it reads.  Refused while the context stream is being captured into a
+ * graph.  Same arguments, results and RawStats as
+ * volta_cuda_pcs_combine_rows_device. */
 int volta_mi355x_pcs_combine_rows_device_noalloc(void* ctx, uint64_t w_id, size_t w_off, uint64_t pads_id,
                                                  size_t pads_off, uint64_t coeffs_id, size_t coeffs_off, size_t rows,
                                                  size_t cols, size_t pad, size_t combinations, uint64_t out_id,
@@ -390,7 +393,13 @@ int volta_mi355x_x4_ntt_fp2_device(void* ctx, uint64_t in_id, size_t in_off, siz
                                    size_t out_off);
 
 /* Device address of a resident byte region / the context stream (a
- * hipStream_t), so a harness can time launches with its own events. */
+ * hipStream_t), so a harness can time launches with its own events.
+ * volta_cuda_pcs_messages_device normally records its rows and lets the
+ * following NTT of exactly those rows encode from the weights and pads; any
+ * access through the ABI writes the rows first.  A raw address bypasses the
+ * ABI, so the query writes pending rows that involve the buffer, and marks the
+ * buffer (until it is freed): a messages call whose output, weights or pads
+ * buffer is marked writes its rows at once, as the reference does. */
 int volta_mi355x_resident_device_ptr(void* ctx, uint64_t id, size_t off_bytes, size_t bytes, void** out);
 int volta_mi355x_stream(void* ctx, void** out);
 int volta_mi355x_synchronize(void* ctx);
@@ -404,6 +413,12 @@ int volta_mi355x_probe_copy_device(void* ctx, uint64_t src_id, uint64_t dst_id, 
  * wave instruction; dst holds 16 x src_bytes. */
 int volta_mi355x_probe_expand_device(void* ctx, uint64_t src_id, uint64_t dst_id, size_t src_bytes);
 int volta_mi355x_probe_fp2_device(void* ctx, uint64_t a_id, uint64_t b_id, uint64_t out_id, size_t n, int rounds);
+
+/* Output checksum of the reference's arithmetic benchmarks over a host array
+ * of n u64 words (cuda/p7_pcs_arithmetic.cu:160-176): for each word x,
+ * h ^= x; h *= 0x100000001B3 (mod 2^64).  Start from h = 0xCBF29CE484222325.
+ * Host only: no context, no device access. */
+uint64_t volta_mi355x_fnv64_host(const uint64_t* v, size_t n, uint64_t h);
 
 #ifdef __cplusplus
 }

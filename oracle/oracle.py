@@ -133,12 +133,28 @@ def _declare(L: ctypes.CDLL) -> None:
         fn.argtypes = args
 
 
-def default_threads() -> int:
-    """Cores available to this process (cgroup/affinity aware)."""
+def cgroup_cpu_quota(path: str = "/sys/fs/cgroup/cpu.max") -> int | None:
+    """Whole CPUs granted by the cgroup v2 quota (floor(quota / period)), or
+    None without a quota: the count scripts/p7_gpu_pcs_arithmetic.py:52-58 of
+    the reference uses for its CPU denominator."""
     try:
-        return max(1, len(os.sched_getaffinity(0)))
+        quota, period = open(path).read().split()[:2]
+    except (OSError, ValueError):
+        return None
+    if quota == "max":
+        return None
+    return max(1, int(quota) // int(period))
+
+
+def default_threads() -> int:
+    """Cores this process may use: the cgroup's CPU quota when one is set,
+    else (and never more than) the CPUs of its affinity mask."""
+    try:
+        affinity = max(1, len(os.sched_getaffinity(0)))
     except AttributeError:  # pragma: no cover
-        return os.cpu_count() or 1
+        affinity = os.cpu_count() or 1
+    quota = cgroup_cpu_quota()
+    return min(quota, affinity) if quota else affinity
 
 
 def _ptr(a: np.ndarray) -> int:

@@ -260,6 +260,23 @@ def test_chacha8_rows_match_fpstream_and_kat(backend, oracle):
     assert (got2 == oracle.fp2_rows_padded(KAT_SEED, 5, 4, 7, 9)).all()
 
 
+# Bernstein ChaCha8, all-zero key and nonce: the published keystream blocks 0
+# and 1.  None of these 16 words is >= p, so FpStream row 0 of the zero seed in
+# domain 0 is exactly that keystream read as little-endian u64.
+ZERO_KEY_BLOCKS_0_1 = bytes.fromhex(
+    "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+    "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42"
+    "d2aefa0deaa5c151bf0adb6c01f2a5adc0fd581259f9a2aadcf20f8fd566a26b"
+    "5032ec38bbc5da98ee0c6f568b872a65a08abf251deb21bb4b56e5d8821e68aa")
+
+
+def test_chacha8_device_rows_published_keystream_two_blocks(backend):
+    d = backend.chacha8_prover_secret_fp_rows_device(bytes(32), 0, 1, 16)
+    got = backend.download_device(d)
+    backend.free_device(d)
+    assert got.astype("<u8").tobytes() == ZERO_KEY_BLOCKS_0_1
+
+
 @pytest.mark.parametrize("count", [6, 8, 511, 512, 1000])
 def test_chacha8_rows_rejection_shifts_later_draws(backend, oracle, count):
     """Rows are filled by one wave, 64 blocks (512 raw draws) per round.  On

@@ -169,3 +169,88 @@ def test_two_recorded_message_calls_and_unrelated_calls_between(backend, oracle)
     for b in (dw, dp, m1, m2, c, u, e1, e2):
         backend.free_device(b)
     assert (got_u == oracle.pcs_combine_rows(w, None, co, rows, cols, pad, 1)).all()
+
+
+def _hip():
+    """The HIP runtime the library already loaded, for copies through raw
+    device addresses (what a harness's own kernels would do)."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so", mode=ctypes.RTLD_GLOBAL)
+    hip.hipMemcpy.restype = ctypes.c_int
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    return hip
+
+
+HIP_H2D, HIP_D2H = 1, 2
+
+
+def test_rows_buffer_address_taken_before_the_messages_call(backend, oracle):
+    """A harness that holds the rows' device address before the messages call
+    can read the rows with its own kernels: the call must write them at once
+    (the buffer is marked by the address query), and the transform then runs
+    on the written rows."""
+    import ctypes
+    rows, cols, pad, n = 8, 2048, 0, 8192
+    w, pads, dw, dp = setup(backend, rows, cols, pad, 61)
+    msgs = backend.alloc_device(rows * n, np.uint64)
+    ptr = backend.device_ptr(msgs)
+    assert backend.lib.volta_cuda_pcs_messages_device(backend.raw, dw.id, 0, dp.id, 0, rows, cols, pad, n, msgs.id,
+                                                      0) == 0, backend.last_error()
+    backend.synchronize()
+    host = np.empty(rows * n, np.uint64)
+    assert _hip().hipMemcpy(host.ctypes.data, ctypes.c_void_p(ptr), host.nbytes, HIP_D2H) == 0
+    enc = backend.ntt_fp_batch_device(msgs, rows, n)
+    got = backend.download_device(enc).reshape(rows, n)
+    for b in (dw, dp, msgs, enc):
+        backend.free_device(b)
+    assert (host.reshape(rows, n) == oracle.pcs_messages(w, pads, rows, cols, pad, n)).all()
+    assert (got == oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)).all()
+
+
+@pytest.mark.parametrize("pad", [0, 512])
+def test_source_address_taken_before_the_messages_call(backend, oracle, pad):
+    """The weights (and pads) overwritten through a raw address after the
+    messages call: the rows are those of the sources at the time of the call,
+    so the call wrote them at once and the transform encodes those rows."""
+    import ctypes
+    rows, cols, n = 6, 2048, 8192 if pad == 0 else 1 << 15
+    w, pads, dw, dp = setup(backend, rows, cols, pad, 71 + pad)
+    wptr = backend.device_ptr(dw)
+    pptr = backend.device_ptr(dp) if pad else None
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, pad, n)
+    backend.synchronize()
+    hip = _hip()
+    junk = rand_i16(99, rows * cols)
+    assert hip.hipMemcpy(ctypes.c_void_p(wptr), junk.ctypes.data, junk.nbytes, HIP_H2D) == 0
+    if pad:
+        junk_p = rand_fp(98, rows * pad)
+        assert hip.hipMemcpy(ctypes.c_void_p(pptr), junk_p.ctypes.data, junk_p.nbytes, HIP_H2D) == 0
+    enc = backend.ntt_fp_batch_device(msgs, rows, n)
+    got = backend.download_device(enc).reshape(rows, n)
+    for b in (dw, dp, msgs, enc):
+        backend.free_device(b)
+    assert (got == oracle.pcs_encode_i16(w, pads if pad else None, rows, cols, pad, n)).all()
+
+
+@pytest.mark.parametrize("bits", [13, 15])
+def test_transform_writing_into_the_pads_buffer(backend, oracle, bits):
+    """Codewords written into the buffer that holds the pads (after them),
+    pad > 0: the fused encode would read the pads while its stores land in
+    the same buffer, so the rows are written and the plain transform runs."""
+    rows, cols, pad, n = 5, 2048, 512, 1 << bits
+    w = rand_i16(81 + bits, rows * cols)
+    pads = rand_fp(82 + bits, rows * pad)
+    dw = backend.upload_device(w)
+    buf = backend.alloc_device(rows * pad + rows * n, np.uint64)  # pads, then the codewords
+    backend.upload_into(buf, 0, pads)
+    msgs = backend.pcs_messages_device(dw, 0, buf, 0, rows, cols, pad, n)
+    assert backend.lib.volta_cuda_ntt_fp_batch_device(backend.raw, msgs.id, 0, rows, n, buf.id, rows * pad) == 0, \
+        backend.last_error()
+    got = backend.download_device(buf, rows * pad, rows * n).reshape(rows, n)
+    left = backend.download_device(buf, 0, rows * pad)
+    got_m = backend.download_device(msgs).reshape(rows, n)
+    for b in (dw, buf, msgs):
+        backend.free_device(b)
+    assert (left == pads).all()
+    assert (got_m == oracle.pcs_messages(w, pads, rows, cols, pad, n)).all()
+    assert (got == oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)).all()

@@ -213,11 +213,17 @@ def test_chacha8_reference_kat(oracle):
 
 
 def test_chacha8_published_zero_key_keystream(oracle):
-    # Bernstein ChaCha, 8 rounds, 256-bit all-zero key, zero nonce, block 0
-    raw = oracle.raw_u64(bytes(32), 0, 8)
-    assert raw.view(np.uint8).tobytes().hex() == (
+    # Bernstein ChaCha, 8 rounds, 256-bit all-zero key, zero nonce: the
+    # published keystream's blocks 0 and 1 (block counter 0 and 1), so the
+    # counter increment and the second block's word order are pinned too.
+    raw = oracle.raw_u64(bytes(32), 0, 16)
+    ks = raw.view(np.uint8).tobytes().hex()
+    assert ks[:128] == (
         "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
         "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42")
+    assert ks[128:] == (
+        "d2aefa0deaa5c151bf0adb6c01f2a5adc0fd581259f9a2aadcf20f8fd566a26b"
+        "5032ec38bbc5da98ee0c6f568b872a65a08abf251deb21bb4b56e5d8821e68aa")
 
 
 def test_stream_domain_separation_and_fp2(oracle):

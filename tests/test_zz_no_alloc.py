@@ -75,3 +75,64 @@ def test_noalloc_combination_refuses_plans_beyond_its_scratch():
         assert not b.download_device(out).view(np.uint64).any()
         for x in (dw, dp, dc, out):
             b.free_device(x)
+
+
+def test_noalloc_combination_two_contexts_back_to_back(oracle):
+    """Two contexts on one GPU share the fixed array: calls from both, issued
+    back to back with no host synchronisation between them, must each give
+    the oracle's combination (the library orders their uses on the device)."""
+    from volta_mi355x import FP2, Backend
+    shapes = [(4096, 2048, 512, 2), (4096, 2048, 0, 2), (2048, 1000, 3, 3)]
+    with Backend() as a, Backend() as b:
+        jobs = []
+        for k, (rows, cols, pad, comb) in enumerate(shapes * 2):
+            ctx = a if k % 2 == 0 else b
+            w = rand_i16(700 + k, rows * cols)
+            pads = rand_fp(710 + k, rows * pad) if pad else np.zeros(1, np.uint64)
+            co = rand_fp(720 + k, (comb * rows, 2))
+            dw, dp, dc = ctx.upload_device(w), ctx.upload_device(pads), ctx.upload_device(co, FP2)
+            out = ctx.alloc_device(comb * (cols + pad), FP2)
+            jobs.append((ctx, w, pads, co, (rows, cols, pad, comb), (dw, dp, dc, out)))
+        a.synchronize()
+        b.synchronize()
+        for ctx, _, _, _, (rows, cols, pad, comb), (dw, dp, dc, out) in jobs:
+            assert call(ctx, "volta_mi355x_pcs_combine_rows_device_noalloc", dw, dp, dc, rows, cols, pad, comb,
+                        out) == 0, ctx.last_error()
+        for ctx, w, pads, co, (rows, cols, pad, comb), bufs in jobs:
+            got = ctx.download_device(bufs[3]).view(np.uint64).reshape(comb, cols + pad, 2)
+            for x in bufs:
+                ctx.free_device(x)
+            assert (got == oracle.pcs_combine_rows(w, pads if pad else None, co, rows, cols, pad, comb)).all(), \
+                (rows, cols, pad, comb)
+
+
+def test_noalloc_combination_refused_during_stream_capture():
+    """While the context stream is being captured the entry point refuses
+    with an error and enqueues nothing (the capture ends with an empty graph)."""
+    import ctypes
+    from volta_mi355x import FP2, Backend
+    hip = ctypes.CDLL("libamdhip64.so", mode=ctypes.RTLD_GLOBAL)
+    hip.hipStreamBeginCapture.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    hip.hipStreamEndCapture.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipGraphDestroy.argtypes = [ctypes.c_void_p]
+    rows, cols, comb = 64, 256, 1
+    with Backend() as b:
+        dw = b.upload_device(rand_i16(5, rows * cols))
+        dp = b.alloc_device(1, np.uint64)
+        dc = b.upload_device(rand_fp(6, (comb * rows, 2)), FP2)
+        out = b.alloc_device(comb * cols, FP2)
+        b.synchronize()
+        s = ctypes.c_void_p(b.stream())
+        assert hip.hipStreamBeginCapture(s, 2) == 0  # hipStreamCaptureModeRelaxed
+        rc = call(b, "volta_mi355x_pcs_combine_rows_device_noalloc", dw, dp, dc, rows, cols, 0, comb, out)
+        err = b.last_error()
+        graph = ctypes.c_void_p()
+        assert hip.hipStreamEndCapture(s, ctypes.byref(graph)) == 0
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        assert rc != 0 and "stream capture" in err
+        # the context works as before once the capture has ended
+        assert call(b, "volta_mi355x_pcs_combine_rows_device_noalloc", dw, dp, dc, rows, cols, 0, comb, out) == 0
+        b.synchronize()
+        for x in (dw, dp, dc, out):
+            b.free_device(x)

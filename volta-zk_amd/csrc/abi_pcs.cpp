@@ -230,9 +230,14 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
         // from the sources: a following forward NTT of exactly these rows
         // (finish_resident_commit, rust/volta-pcs/src/ligero.rs:477-496) then
         // encodes straight from the weights and pads, and any other access
-        // writes them first (settle_pending).  The stats are those of a
-        // messages call either way.
-        if (out_id != w_id && (!pad || out_id != pads_id)) {
+        // writes them first (settle_pending).  They are written at once when
+        // the caller holds the device address of the rows' buffer or of a
+        // source (volta_mi355x_resident_device_ptr), since its own kernels
+        // could read the rows or change a source behind the library.  The
+        // stats are those of a messages call either way.
+        const bool exposed = find_resident(c, out_id)->exposed || find_resident(c, w_id)->exposed ||
+                             (pad && find_resident(c, pads_id)->exposed);
+        if (!exposed && out_id != w_id && (!pad || out_id != pads_id)) {
             if (c->has_pending && settle_pending(c)) return -1;  // one record at a time
             c->pending = PendingMessages{out_id, out_off, static_cast<uint64_t*>(out), w_id, pad ? pads_id : 0,
                                          static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
@@ -283,12 +288,15 @@ VMX_API int volta_cuda_pcs_combine_rows_device(void* raw, uint64_t w_id, size_t 
 }
 
 // volta_cuda_pcs_combine_rows_device without allocation, for callers that
-// cannot allocate (code under HIP graph capture, serving loops): the partials
-// and coefficient sums live in a fixed 16 MiB device array per GPU instead of
-// the context's grow-only workspaces, and a plan that needs more is refused
-// with an error.  All calls on one GPU share that array, so calls that overlap
-// in time on one GPU (several contexts or threads) race; each call rewrites
-// every scratch word it reads.  Same arguments, results and stats.
+// cannot allocate (serving loops, harnesses that forbid hipMalloc): the
+// partials and coefficient sums live in a fixed 16 MiB device array per GPU
+// instead of the context's grow-only workspaces, and a plan that needs more is
+// refused with an error.  All contexts on one GPU share that array; their uses
+// are ordered on the device by a per-device event (each use waits for the
+// previous one), and each call rewrites every scratch word it reads.  It is
+// refused while the context stream is being captured into a graph: its timing
+// may synchronise the stream and its ordering event comes from outside the
+// capture.  Same arguments, results and stats.
 VMX_API int volta_mi355x_pcs_combine_rows_device_noalloc(void* raw, uint64_t w_id, size_t w_off, uint64_t pads_id,
                                                           size_t pads_off, uint64_t co_id, size_t co_off, size_t rows,
                                                           size_t cols, size_t pad, size_t combinations,
@@ -296,6 +304,10 @@ VMX_API int volta_mi355x_pcs_combine_rows_device_noalloc(void* raw, uint64_t w_i
     Context* c = static_cast<Context*>(raw);
     if (!c || !rows || !cols || !combinations) return fail_msg(c, "invalid resident PCS combination geometry");
     return guarded(c, "allocation-free resident PCS combination", [&] {
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        VMX_HIP(c, hipStreamIsCapturing(c->stream, &cap));
+        if (cap != hipStreamCaptureStatusNone)
+            return fail_msg(c, "allocation-free PCS combination is refused during stream capture");
         return combine_device(c, w_id, w_off, pads_id, pads_off, co_id, co_off, rows, cols, pad, combinations,
                               out_id, out_off, true);
     });
@@ -584,11 +596,16 @@ VMX_API int volta_mi355x_combine_rows_fp_device(void* raw, uint64_t m_id, size_t
 }
 
 // Raw device address of a resident region, for measurement harnesses that
-// time kernels with their own events on the context stream.
+// time kernels with their own events on the context stream.  Deferred message
+// rows that involve the buffer are written first (region), and the buffer is
+// marked exposed for the rest of its allocation: no later messages call defers
+// rows that live in it or are made from it.
 VMX_API int volta_mi355x_resident_device_ptr(void* raw, uint64_t id, size_t off_bytes, size_t bytes, void** out) {
     Context* c = static_cast<Context*>(raw);
     if (!c || !out) return fail_msg(c, "invalid device-pointer query");
-    return region(c, id, off_bytes, bytes, out);
+    if (region(c, id, off_bytes, bytes, out)) return -1;
+    find_resident(c, id)->exposed = true;
+    return 0;
 }
 
 // The context's HIP stream (hipStream_t), for event timing by a harness.
@@ -597,6 +614,18 @@ VMX_API int volta_mi355x_stream(void* raw, void** out) {
     if (!c || !out) return fail_msg(c, "invalid stream query");
     *out = c->stream;
     return 0;
+}
+
+// The output checksum of the reference's arithmetic benchmarks
+// (cuda/p7_pcs_arithmetic.cu:160-176): h ^= x; h *= 0x100000001B3 over u64
+// words, a host loop over a host array (the words are read in order).
+VMX_API uint64_t volta_mi355x_fnv64_host(const uint64_t* v, size_t n, uint64_t h) {
+    if (!v) return h;
+    for (size_t i = 0; i < n; ++i) {
+        h ^= v[i];
+        h *= 0x00000100000001B3ull;
+    }
+    return h;
 }
 
 // Measurement probes: streaming copy (achievable HBM bandwidth) and the

@@ -1074,6 +1074,7 @@ VMX_API int volta_cuda_resident_alloc(void* raw, size_t bytes, uint64_t* out_id)
     r.capacity = bytes;
     r.logical = bytes;
     r.active = true;
+    r.exposed = false;
     *out_id = make_id(slot, r.generation);
     return 0;
     VMX_GUARD_END(c, "resident allocation")

@@ -141,6 +141,10 @@ struct Resident {
     size_t logical = 0;
     uint32_t generation = 0;
     bool active = false;
+    // Its device address was handed to the caller (volta_mi355x_resident_device_ptr):
+    // the caller's own kernels may read or write it outside the library, so no
+    // deferred message rows involve it.
+    bool exposed = false;
 };
 
 struct Pinned {

@@ -44,8 +44,52 @@ __host__ __device__ __forceinline__ uint64_t sub(uint64_t a, uint64_t b) {
 
 __host__ __device__ __forceinline__ uint64_t neg(uint64_t a) { return a ? P - a : 0; }
 
-// Fold a 128-bit value (hi:lo) to a canonical element.
-__host__ __device__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
+// Fold a 128-bit value (hi:lo) to a canonical element:
+// hi:lo = lo + hl 2^64 + hh 2^96 = lo + hl eps - hh (mod p).
+#if defined(__HIP_DEVICE_COMPILE__)
+// gfx950: t = lo - hh (mod p) as a borrow chain; then one v_mad_u64_u32
+// forms r = t + hl eps and its carry out of 2^64, which the compiler has no
+// way to read (it would recompute the product and compare).  A carry is
+// worth eps, and r < 2^64 - 2^33 + 1 when it is set, so r + eps is then
+// already canonical; without it r + eps is r - p exactly when r >= p, which
+// the carry out of r + eps reports.  Hence the result is r + eps when either
+// carry is set, else r: 10 VALU instructions and one SALU or, against 16.
+// The s_nop lines are the two wait states gfx950 needs between a VALU write
+// of VCC and a VALU read of it (the compiler inserts the same); a SALU read
+// of a VALU-written mask and a VALU read of a SALU-written one need none.
+__device__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
+    const uint32_t hh = static_cast<uint32_t>(hi >> 32), hl = static_cast<uint32_t>(hi);
+    // t = lo - hh, and eps less when that borrows (t stays >= 0 then)
+    uint32_t t0, t1, e;
+    asm("v_sub_co_u32 %0, vcc, %3, %5\n\t"
+        "s_nop 1\n\t"
+        "v_subbrev_co_u32 %1, vcc, 0, %4, vcc\n\t"
+        "s_nop 1\n\t"
+        "v_cndmask_b32 %2, 0, -1, vcc\n\t"
+        "v_sub_co_u32 %0, vcc, %0, %2\n\t"
+        "s_nop 1\n\t"
+        "v_subbrev_co_u32 %1, vcc, 0, %1, vcc"
+        : "=&v"(t0), "=&v"(t1), "=&v"(e)
+        : "v"(static_cast<uint32_t>(lo)), "v"(static_cast<uint32_t>(lo >> 32)), "v"(hh)
+        : "vcc");
+    const uint64_t t = (static_cast<uint64_t>(t1) << 32) | t0;
+    uint64_t r, c;
+    asm("v_mad_u64_u32 %0, %1, %2, -1, %3" : "=v"(r), "=s"(c) : "v"(hl), "v"(t));
+    const uint32_t r0 = static_cast<uint32_t>(r), r1 = static_cast<uint32_t>(r >> 32);
+    uint32_t s0, s1;
+    asm("v_add_co_u32 %0, vcc, -1, %2\n\t"
+        "s_nop 1\n\t"
+        "v_addc_co_u32 %1, vcc, 0, %3, vcc\n\t"
+        "s_or_b64 vcc, vcc, %4\n\t"
+        "v_cndmask_b32 %0, %2, %0, vcc\n\t"
+        "v_cndmask_b32 %1, %3, %1, vcc"
+        : "=&v"(s0), "=&v"(s1)
+        : "v"(r0), "v"(r1), "s"(c)
+        : "vcc", "scc");
+    return (static_cast<uint64_t>(s1) << 32) | s0;
+}
+#else
+__host__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
     const uint64_t hh = hi >> 32;
     const uint64_t hl = hi & EPS;
     uint64_t t = lo - hh;               // lo - hh*2^96
@@ -55,6 +99,7 @@ __host__ __device__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
     r += (r < m) ? EPS : 0;             // carry of 2^64 = eps
     return r >= P ? r - P : r;
 }
+#endif
 
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ __forceinline__ void mul_wide(uint64_t a, uint64_t b, uint64_t& lo, uint64_t& hi) {

@@ -481,26 +481,38 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const F
 // pcs_combine_rows_noalloc, so that entry point allocates nothing.  Host code
 // never uses the array's name as an address: combine_scratch_attach resolves
 // this device's copy once (hipGetSymbolAddress, with the device current) and
-// every launch takes that pointer.  All calls on one GPU share its array.
+// every launch takes that pointer.  All contexts on one GPU share its array:
+// each use records a per-device event after its last launch, and the next use
+// (from any context of that device) makes its own stream wait on that event
+// first, so uses on one GPU run one after another on the device.
 static __device__ __align__(256) unsigned char combine_scratch[COMBINE_SCRATCH_BYTES];
 
+namespace {
+struct ScratchDevice {
+    void* ptr = nullptr;
+    hipEvent_t last = nullptr;  // recorded after the latest use's launches
+    bool used = false;
+};
+std::mutex scratch_mu;
+std::map<int, ScratchDevice> scratch_by_device;  // each device's copy of combine_scratch
+}  // namespace
+
 int combine_scratch_attach(Context* c) {
-    static std::mutex mu;
-    static std::map<int, void*> by_device;  // each device's address of combine_scratch
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = by_device.find(c->device);
-    if (it == by_device.end()) {
-        void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(combine_scratch));
-        if (e != hipSuccess || !p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    auto it = scratch_by_device.find(c->device);
+    if (it == scratch_by_device.end()) {
+        ScratchDevice d;
+        hipError_t e = hipGetSymbolAddress(&d.ptr, HIP_SYMBOL(combine_scratch));
+        if (e == hipSuccess && d.ptr) e = hipEventCreateWithFlags(&d.last, hipEventDisableTiming);
+        if (e != hipSuccess || !d.ptr) {
             c->scratch = nullptr;
-            c->scratch_error = std::string("hipGetSymbolAddress(combine_scratch) failed: ") +
+            c->scratch_error = std::string("resolving combine_scratch failed: ") +
                                (e != hipSuccess ? hipGetErrorString(e) : "null address");
             return -1;
         }
-        it = by_device.emplace(c->device, p).first;
+        it = scratch_by_device.emplace(c->device, d).first;
     }
-    c->scratch = it->second;
+    c->scratch = it->second.ptr;
     return 0;
 }
 
@@ -519,9 +531,16 @@ int pcs_combine_rows_noalloc(Context* c, const int16_t* w, const uint64_t* pads,
         return fail_msg(c, m.c_str());
     }
     unsigned char* base = static_cast<unsigned char*>(c->scratch);
-    return combine_launch(c, w, pads, coeffs, rows, cols, pad, combinations, out, pl,
-                          pl.part_bytes ? reinterpret_cast<Fp2*>(base) : nullptr,
-                          reinterpret_cast<uint64_t*>(base + part_span));
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    ScratchDevice& d = scratch_by_device.at(c->device);
+    if (d.used) VMX_HIP(c, hipStreamWaitEvent(c->stream, d.last, 0));
+    if (combine_launch(c, w, pads, coeffs, rows, cols, pad, combinations, out, pl,
+                       pl.part_bytes ? reinterpret_cast<Fp2*>(base) : nullptr,
+                       reinterpret_cast<uint64_t*>(base + part_span)))
+        return -1;
+    VMX_HIP(c, hipEventRecord(d.last, c->stream));
+    d.used = true;
+    return 0;
 }
 
 int combine_rows_fp(Context* c, const uint64_t* m, size_t rows, size_t cols, const Fp2* coeffs,

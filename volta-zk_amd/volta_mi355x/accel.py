@@ -158,6 +158,7 @@ _SIGS = {
     "volta_mi355x_probe_copy_device": (_int, [_vp, _u64, _u64, _sz]),
     "volta_mi355x_probe_expand_device": (_int, [_vp, _u64, _u64, _sz]),
     "volta_mi355x_probe_fp2_device": (_int, [_vp, _u64, _u64, _u64, _sz, _int]),
+    "volta_mi355x_fnv64_host": (_u64, [_vp, _sz, _u64]),
 }
 
 
