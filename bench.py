@@ -229,8 +229,11 @@ def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
     `fused`: the calls as Rust makes them, the rows' buffer allocated before
     and freed after (the rows stay unwritten and the transform encodes from
     the weights); `written`: the same calls with the rows forced into HBM
-    before the transform (a device-pointer query of their buffer), i.e. the
-    chain without the deferral."""
+    before the transform by a device-pointer query of their buffer (the
+    caller may then write the rows itself, so the transform reads them whole:
+    the chain without the deferral); `written_read_back`: the rows forced into
+    HBM by reading 8 bytes of them back (the library wrote them and nothing
+    else has, so the transform reads only their nonzero part)."""
     import numpy as np
     if wl.name not in ("c2", "c3"):
         return None
@@ -238,18 +241,22 @@ def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
     rows, n = cfg.rows, cfg.n
     L, r = b.lib, b.raw
 
+    probe = np.empty(1, np.uint64)
+
     def chain(force):
         m = wl.messages_buffer(rows * n * 8)
         wl._ok(L.volta_cuda_pcs_messages_device(r, wl.w.id, 0, wl.pads.id, 0, rows, cfg.msg_len, 0, n, m, 0))
-        if force:
+        if force == "written":
             p = ctypes.c_void_p()
             wl._ok(L.volta_mi355x_resident_device_ptr(r, m, 0, 8, ctypes.byref(p)))
+        elif force == "written_read_back":
+            wl._ok(L.volta_cuda_resident_download(r, m, 0, probe.ctypes.data, 8))
         wl._ok(L.volta_cuda_ntt_fp_batch_device(r, m, 0, rows, n, wl.enc.id, 0))
         wl._ok(L.volta_cuda_resident_free(r, m))
 
     out = {"calls": "volta_cuda_pcs_messages_device + volta_cuda_ntt_fp_batch_device", "rows": rows,
            "code_len": n, "algorithmic_bytes": cfg.algorithmic_bytes, "reps": reps}
-    for force in (False, True):
+    for force in ("fused", "written", "written_read_back"):
         for _ in range(2):
             chain(force)
         b.synchronize()
@@ -261,8 +268,7 @@ def seam_chain(b, wl: "Workload", reps: int = 10) -> dict | None:
         wall = (time.perf_counter() - t0) / reps
         s = b.get_stats()
         ntt_ms = s["kernel_ns"]["pcs_ntt"] / reps / 1e6
-        key = "written" if force else "fused"
-        out[key] = {"ms_per_chain": round(wall * 1e3, 4), "ntt_call_ms": round(ntt_ms, 4),
+        out[force] = {"ms_per_chain": round(wall * 1e3, 4), "ntt_call_ms": round(ntt_ms, 4),
                     "messages_call_ms": round(s["kernel_ns"]["pcs_rows"] / reps / 1e6, 4),
                     "achieved_gbs": round(cfg.algorithmic_bytes / wall / 1e9, 1),
                     "frac_of_peak": round(cfg.algorithmic_bytes / wall / 1e9 / HBM_PEAK_GBS, 4)}
@@ -361,6 +367,50 @@ def published_shapes(b, reps: int = 10) -> dict:
         "checksum_expected": "0x856f9a96d8e01901", "reference_a100_ms": 1.918,
         "speedup_vs_reference_a100": round(1.918 / ms, 1)}
     return out
+
+
+def host_batch(b, wl: "Workload", reps: int = 3) -> dict | None:
+    """The hybrid commit's transform (rust/volta-pcs/src/ligero.rs:564-581 ->
+    Backend::ntt_fp_batch, rust/volta-accel/src/lib.rs:4722-4746): compact
+    host rows lift(w) of msg_len u64 in, rows x n codewords back to host
+    memory, through volta_cuda_ntt_fp_batch at the workload's shape.  Timed
+    with the library's events (kernel, upload, download) and the wall clock
+    around the call; the codewords must equal the resident encode's of the
+    same weights (sampled rows), or the leg raises.  Not part of `value`."""
+    import numpy as np
+    if wl.name not in ("c2", "c3"):
+        return None
+    cfg = wl.cfg
+    rows, n, m = cfg.rows, cfg.n, cfg.msg_len
+    w = wl.host_w.reshape(rows, m)
+    # Fp::from_i64 (rust/volta-field/src/lib.rs:32-40): x < 0 -> p - |x| = (2^64 + x) - (2^32 - 1)
+    msgs = w.astype(np.int64).astype(np.uint64)
+    neg = w < 0
+    msgs[neg] -= np.uint64(0xFFFF_FFFF)
+    del neg
+    out = np.empty((rows, n), np.uint64)
+    L, r = b.lib, b.raw
+    call = lambda: b._check(L.volta_cuda_ntt_fp_batch(r, msgs.ctypes.data, rows, m, n, out.ctypes.data))
+    call()
+    b.reset_stats()
+    walls = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        call()
+        walls.append(time.perf_counter() - t0)
+    s = b.get_stats()
+    pick = [0, rows // 3, rows - 1]
+    ref = np.stack([b.download_device(wl.enc, i * n, n) for i in pick])
+    if not (out[pick] == ref).all():
+        raise RuntimeError("host batch NTT differs from the resident encode of the same weights")
+    kern = s["kernel_ns"]["pcs_ntt"] / reps / 1e6
+    return {"call": "volta_cuda_ntt_fp_batch (compact host rows lift(w), msg_len per row)", "rows": rows,
+            "msg_len": m, "n": n, "reps": reps, "kernel_ms": round(kern, 4),
+            "h2d_ms": round(s["h2d_ns"] / reps / 1e6, 3), "d2h_ms": round(s["d2h_ns"] / reps / 1e6, 3),
+            "wall_ms_per_call": round(statistics.median(walls) * 1e3, 2),
+            "kernel_gelem_per_s": round(rows * n / kern / 1e6, 1),
+            "note": "the wall time holds the PCIe copies of 8 B per message element in and 8 B per codeword "
+                    "element out to pageable host memory"}
 
 
 def fp2_chain_peak(b, log_n: int = 20, rounds: int = 256, reps: int = 10) -> dict:
@@ -708,6 +758,7 @@ def main() -> int:
     ap.add_argument("--no-seam-chain", action="store_true")
     ap.add_argument("--no-reference-commits", action="store_true")
     ap.add_argument("--no-published-shapes", action="store_true")
+    ap.add_argument("--no-host-batch", action="store_true")
     ap.add_argument("--x4-log-n", type=int, default=24)
     a = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -751,6 +802,10 @@ def main() -> int:
     if not a.no_seam_chain:
         log("seam chain (messages + NTT through the reference's calls)")
         chain_leg = seam_chain(b, wl)
+    hbatch = None
+    if not a.no_host_batch:
+        log("host batch NTT (the hybrid commit's volta_cuda_ntt_fp_batch) at the workload's shape")
+        hbatch = host_batch(b, wl)
     shapes = None
     if not a.no_published_shapes:
         log("the reference's published shapes (P4_LAYER NTT, 1024 x 16384 two-combination)")
@@ -809,6 +864,7 @@ def main() -> int:
         "x4": x4,
         "reference_commits": commits,
         "reference_published_shapes": shapes,
+        "host_batch": hbatch,
     }
     print(json.dumps(out), flush=True)
     return 0

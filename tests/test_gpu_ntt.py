@@ -430,17 +430,26 @@ def test_c2_full_config(backend, oracle):
     assert (got == oracle.pcs_encode_i16(w, None, cfg.rows, cfg.msg_len, 0, cfg.n)).all()
 
 
-def test_c3_full_config_every_row(backend, oracle):
+@pytest.mark.parametrize("path", ["reference_chain", "fused_entry"])
+def test_c3_full_config_every_row(backend, oracle, path):
     """C3 at full size (2^16 rows of 2^11 i16 -> 2^13): every codeword element
     against the oracle, in blocks of 8192 rows (the oracle, threaded, redoes
     the whole encode in seconds), and the whole output once more by a linear
     invariant: the sum of all codewords equals the encode of the sum of all
-    messages."""
+    messages.  Through the reference's two calls as the bench times them
+    (pcs_messages_device into a fresh buffer, ntt_fp_batch_device of those
+    rows, the rows freed unread: finish_resident_commit, ligero.rs:477-496) and
+    through the fused extension entry point."""
     from volta_mi355x import workloads as W
     cfg = W.CONFIGS["c3"]
     w = W.c3_weights()
     dw, dp = backend.upload_device(w.reshape(-1)), backend.alloc_device(1, np.uint64)
-    out = backend.pcs_encode_device(dw, 0, dp, 0, cfg.rows, cfg.msg_len, 0, cfg.n)
+    if path == "reference_chain":
+        msgs = backend.pcs_messages_device(dw, 0, dp, 0, cfg.rows, cfg.msg_len, 0, cfg.n)
+        out = backend.ntt_fp_batch_device(msgs, cfg.rows, cfg.n)
+        backend.free_device(msgs)
+    else:
+        out = backend.pcs_encode_device(dw, 0, dp, 0, cfg.rows, cfg.msg_len, 0, cfg.n)
     block = 8192
     for r0 in range(0, cfg.rows, block):
         got = backend.download_device(out, r0 * cfg.n, block * cfg.n).reshape(block, cfg.n)
@@ -486,3 +495,48 @@ def test_c5_rows_forward_inverse(backend, oracle):
         backend.free_device(b)
     assert (back == host).all()
     assert (got == oracle.ntt_forward_batch(host)).all()
+
+
+# ---- n = 2^13 in one pass: written u64 rows and the host batch -------------------------
+
+@pytest.mark.parametrize("rows", [1, 3, 64, 513, 1031])
+def test_ntt13_one_pass_device_rows(backend, oracle, rows):
+    """volta_cuda_ntt_fp_batch_device at n = 2^13 on arbitrary canonical rows
+    (the rows a caller wrote: every column input can be nonzero), as many
+    rows as workgroups and more (the persistent grid walks them), boundary
+    values included, with element offsets on both sides."""
+    n = 1 << 13
+    host = rand_fp(1300 + rows, (rows, n))
+    host[0, :6] = [0, 1, P - 1, P - 2, 1 << 32, (1 << 63) + 5]
+    if rows > 2:
+        host[1] = P - 1
+        host[2] = 0
+    off_in, off_out = 24, 40
+    din = backend.alloc_device(off_in + rows * n, np.uint64)
+    backend.upload_into(din, off_in, host.reshape(-1))
+    dout = backend.alloc_device(off_out + rows * n, np.uint64)
+    assert backend.lib.volta_cuda_ntt_fp_batch_device(backend.raw, din.id, off_in, rows, n, dout.id, off_out) == 0, \
+        backend.last_error()
+    got = backend.download_device(dout, off_out, rows * n).reshape(rows, n)
+    kept = backend.download_device(din, off_in, rows * n).reshape(rows, n)
+    for b in (din, dout):
+        backend.free_device(b)
+    assert (kept == host).all()  # input preserved
+    want = oracle.ntt_forward_batch(host)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
+
+
+@pytest.mark.parametrize("msg_len", [1, 5, 2047, 2048, 2049, 4096, 8191, 8192])
+def test_ntt13_one_pass_host_batch_lengths(backend, oracle, msg_len):
+    """The host batch (volta_cuda_ntt_fp_batch, compact rows of msg_len, the
+    hybrid commit's call, rust/volta-pcs/src/ligero.rs:564-581) at n = 2^13 on
+    both sides of the zero-tail switch (msg_len <= 2048 reads one input of
+    each four per column)."""
+    n, rows = 1 << 13, 37
+    host = rand_fp(1400 + msg_len, (rows, msg_len))
+    host[0, 0] = P - 1
+    got = backend.ntt_fp_batch(host, rows, msg_len, n)
+    padded = np.zeros((rows, n), np.uint64)
+    padded[:, :msg_len] = host
+    assert (got == oracle.ntt_forward_batch(padded)).all()

@@ -254,3 +254,28 @@ def test_transform_writing_into_the_pads_buffer(backend, oracle, bits):
     assert (left == pads).all()
     assert (got_m == oracle.pcs_messages(w, pads, rows, cols, pad, n)).all()
     assert (got == oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)).all()
+
+
+@pytest.mark.parametrize("rows,cols,pad,bits", [(16, 2048, 0, 13), (6, 2048, 512, 13), (4, 8192, 512, 15)])
+def test_written_rows_transform_and_a_later_write_into_their_tail(backend, oracle, rows, cols, pad, bits):
+    """Rows read back before the transform are written by the library, which
+    then knows their zero tail and transforms only their nonzero prefix; an
+    upload into a tail afterwards (any write to the buffer) ends that
+    knowledge, and the next transform reads the whole rows."""
+    n = 1 << bits
+    w, pads, dw, dp = setup(backend, rows, cols, pad, 90 + bits + pad)
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, pad, n)
+    part = backend.download_device(msgs, 0, 8)  # a read: the rows are written now
+    enc1 = backend.ntt_fp_batch_device(msgs, rows, n)
+    want_m = oracle.pcs_messages(w, pads if pad else None, rows, cols, pad, n)
+    tail = rand_fp(91, 5)
+    backend.upload_into(msgs, (rows - 1) * n + n - 5, tail)  # into the last row's zero tail
+    enc2 = backend.ntt_fp_batch_device(msgs, rows, n)
+    got1 = backend.download_device(enc1).reshape(rows, n)
+    got2 = backend.download_device(enc2).reshape(rows, n)
+    for b in (dw, dp, msgs, enc1, enc2):
+        backend.free_device(b)
+    assert (part == want_m.reshape(-1)[:8]).all()
+    assert (got1 == oracle.ntt_forward_batch(want_m)).all()
+    want_m[rows - 1, n - 5:] = tail
+    assert (got2 == oracle.ntt_forward_batch(want_m)).all()

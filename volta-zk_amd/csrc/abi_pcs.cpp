@@ -104,11 +104,18 @@ VMX_API int volta_cuda_ntt_fp_batch_device(void* raw, uint64_t in_id, size_t in_
             return encode_pending(c, pm, static_cast<uint64_t*>(out));
         }
         void *in = nullptr, *out = nullptr;
-        if (region_elems(c, in_id, in_off, total, 8, &in, true) || region_elems(c, out_id, out_off, total, 8, &out))
-            return -1;
+        if (region_elems(c, in_id, in_off, total, 8, &in, true)) return -1;
+        // Rows the library wrote as messages (and nothing has touched since
+        // but reads) are zero from cols + pad on: the transform reads only
+        // that prefix of each row.
+        size_t len = n;
+        if (const Resident* rr = find_resident(c, in_id); rr && rr->msg_rows && rr->msg_off == in_off &&
+                                                          rr->msg_count == rows && rr->msg_row_len == n)
+            len = rr->msg_nonzero;
+        if (region_elems(c, out_id, out_off, total, 8, &out)) return -1;
         if (in_id == out_id && in_off < out_off + total && out_off < in_off + total)
             return fail_msg(c, "resident Fp NTT input and output overlap");
-        return resident_ntt(c, static_cast<const uint64_t*>(in), n, n, rows, n, static_cast<uint64_t*>(out),
+        return resident_ntt(c, static_cast<const uint64_t*>(in), n, len, rows, n, static_cast<uint64_t*>(out),
                             false);
     });
 }
@@ -243,9 +250,12 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
                                          static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
                                          rows, cols, pad, code_len};
             c->has_pending = true;
-        } else if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols,
-                                pad, code_len, static_cast<uint64_t*>(out))) {
-            return -1;
+        } else {
+            if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols, pad,
+                             code_len, static_cast<uint64_t*>(out)))
+                return -1;
+            if (out_id != w_id && (!pad || out_id != pads_id))
+                note_message_rows(c, out_id, out_off, rows, code_len, cols + pad);
         }
         if (mark_op(c, 2)) return -1;
         return finish_op(c, OP_PCS_ROWS, 0, 0);

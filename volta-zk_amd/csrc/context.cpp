@@ -95,11 +95,23 @@ Resident* find_resident(Context* c, uint64_t id) {
     return (r.active && r.generation == gen) ? &r : nullptr;
 }
 
+void note_message_rows(Context* c, uint64_t id, size_t off, size_t rows, size_t row_len, size_t nonzero) {
+    Resident* r = find_resident(c, id);
+    if (!r || r->exposed) return;
+    r->msg_rows = true;
+    r->msg_off = off;
+    r->msg_count = rows;
+    r->msg_row_len = row_len;
+    r->msg_nonzero = nonzero;
+}
+
 int settle_pending(Context* c) {
     if (!c->has_pending) return 0;
     const PendingMessages m = c->pending;
     c->has_pending = false;
-    return pcs_messages(c, m.w, m.pads, m.rows, m.cols, m.pad, m.code_len, m.out);
+    if (pcs_messages(c, m.w, m.pads, m.rows, m.cols, m.pad, m.code_len, m.out)) return -1;
+    note_message_rows(c, m.out_id, m.out_off, m.rows, m.code_len, m.cols + m.pad);
+    return 0;
 }
 
 // Every entry point reaches resident memory through region(), so deferred
@@ -118,6 +130,7 @@ int region(Context* c, uint64_t id, size_t offset_bytes, size_t bytes, void** ou
     if (!r) return fail_msg(c, "unknown resident buffer id");
     if (offset_bytes > r->logical || bytes > r->logical - offset_bytes)
         return fail_msg(c, "resident buffer region is out of bounds");
+    if (!read_only) r->msg_rows = false;  // anything but a read may change the recorded rows
     *out = static_cast<unsigned char*>(r->ptr) + offset_bytes;
     return 0;
 }
@@ -1033,6 +1046,8 @@ VMX_API int volta_cuda_resident_alloc(void* raw, size_t bytes, uint64_t* out_id)
         ++r.generation;
         r.logical = bytes;
         r.active = true;
+        r.exposed = false;   // a new allocation: nothing is known of its contents
+        r.msg_rows = false;
         ++c->stats.resident_reuse_hits;
         *out_id = make_id(best, r.generation);
         return 0;
@@ -1075,6 +1090,7 @@ VMX_API int volta_cuda_resident_alloc(void* raw, size_t bytes, uint64_t* out_id)
     r.logical = bytes;
     r.active = true;
     r.exposed = false;
+    r.msg_rows = false;
     *out_id = make_id(slot, r.generation);
     return 0;
     VMX_GUARD_END(c, "resident allocation")
@@ -1100,6 +1116,8 @@ VMX_API int volta_cuda_resident_free(void* raw, uint64_t id) {
     c->free_slots.push_back(static_cast<size_t>((id & 0xFFFFFFFFull) - 1));
     r->logical = 0;
     r->active = false;
+    r->exposed = false;
+    r->msg_rows = false;
     return 0;
     VMX_GUARD_END(c, "resident free")
 }

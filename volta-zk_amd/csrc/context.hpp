@@ -145,6 +145,13 @@ struct Resident {
     // the caller's own kernels may read or write it outside the library, so no
     // deferred message rows involve it.
     bool exposed = false;
+    // Message rows lift(w) || pads || 0 that the library itself wrote here
+    // (rows of row_len elements from element off, zero from element nonzero
+    // on in each row), kept until anything other than a read touches the
+    // buffer: a forward NTT of exactly those rows then reads only the nonzero
+    // part.
+    bool msg_rows = false;
+    size_t msg_off = 0, msg_count = 0, msg_row_len = 0, msg_nonzero = 0;
 };
 
 struct Pinned {
@@ -307,6 +314,9 @@ int pinned_mark_in_flight(Context* c, Pinned* p);
 // Writes the deferred message rows, if any (one launch on the context stream,
 // outside any primitive's timing record).
 int settle_pending(Context* c);
+// Records that buffer `id` holds message rows the library wrote (Resident::msg_rows);
+// nothing is recorded for a buffer whose address the caller holds.
+void note_message_rows(Context* c, uint64_t id, size_t off, size_t rows, size_t row_len, size_t nonzero);
 
 // ---- workspaces and twiddles ---------------------------------------------------
 int ensure_ws(Context* c, int slot, size_t bytes);

@@ -59,6 +59,23 @@ __host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1
     });
 }
 
+// Phase B of one row: the 64-point DFT over i2 of Y's row j1 at output parity
+// H, X[2k + H] stored to o[j1 + N1 (2k + H)].  The workgroup's second barrier
+// sits between the LDS reads and the DFT: Y is rewritten by the next row's
+// phase A, and once every wave holds its rows' first stage in registers the
+// workgroup may move on, so the DFTs and stores overlap the next phase A of
+// faster waves.
+__device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, int H, uint64_t* o) {
+    uint64_t v[K];
+    if (H == 0) phase_b_first<0>(Y, j1, v);
+    else phase_b_first<1>(Y, j1, v);
+    __syncthreads();
+    gl::dit_pow2<5, gl::E_W32>(v);
+    o += j1 + N1 * H;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);
+}
+
 // The row's inputs as the matrix product's B operand: lane l, column tile t
 // holds x[64 i1 + 16 t + (l & 15)] for i1 in [8 (l >> 4), 8 (l >> 4) + 8), two
 // per word as the digit pairs x ^ 0x80 (low byte (x & 255) - 128, high byte
@@ -183,17 +200,7 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
         if (next < rows) load_frags(w + next * cols, cols, lane, xf);
         __syncthreads();
         __builtin_amdgcn_s_setprio(0);
-        uint64_t v[K];
-        if (H == 0) phase_b_first<0>(Y, j1b, v);
-        else phase_b_first<1>(Y, j1b, v);
-        // Y is rewritten by the next row's phase A.  Once every wave holds its
-        // rows' first stage in registers the workgroup may move on, so the
-        // DFTs and stores of phase B overlap the next phase A of faster waves.
-        __syncthreads();
-        gl::dit_pow2<5, gl::E_W32>(v);
-        uint64_t* o = out + row * N + j1b + N1 * H;
-#pragma unroll
-        for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);
+        phase_b(Y, j1b, H, out + row * N);
         H ^= 1;
     }
 }
@@ -207,6 +214,103 @@ __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __rest
     const v4i* init = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(frags) + enc13m::FRAG_BYTES);
     encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane, k16,
                 keps);
+}
+
+// ---- zero-tailed u64 rows: the same split with phase A on the VALU -------------------
+// Forward NTT of rows of n = 2^13 canonical elements that are zero from
+// element 2^11 on, in one pass: the compact rows of the host batch
+// (msg_len <= 2048) and message rows the library wrote itself, whose zero
+// tail it knows.  With the inputs x[64 a + i2] (a < 32) nonzero, phase A's
+// 128-point column DFTs run on the VALU, one coset of outputs j1 = C + 4 j'
+// per wave and one column i2 per lane:
+//   X[C + 4 j'][i2] = sum_{a < 32} w32^(a j') (w128^(a C) x[64 a + i2]),
+// the pre-twiddle w128^(a C) (a shift for even a C, two shifts and a
+// subtract for odd: w128 = 2^43 - 2^91), one 32-point shift-only DFT over a,
+// then the twiddle w^(i2 j1) into Y.  Phase B is the encode's.  The four
+// cosets share one code path (uniform branches on the coset's two bits,
+// w128^(a C) = w128^(a (C & 1)) w64^(a (C >> 1))), which keeps the kernel
+// within the instruction cache.
+
+// x w128^K for canonical x (any K >= 0).
+template <int K>
+__device__ __forceinline__ uint64_t mul_w128(uint64_t x) {
+    constexpr int k = K % 128;
+    if constexpr (k % 2 == 0) {
+        return gl::mul_pow2<gl::E_W64 * (k / 2)>(x);
+    } else {
+        constexpr int c = gl::E_W64 * ((k - 1) / 2);
+        return gl::sub(gl::mul_pow2<43 + c>(x), gl::mul_pow2<91 + c>(x));
+    }
+}
+
+__device__ __forceinline__ uint64_t load_u64(const __amdgpu_buffer_rsrc_t& r, int voff, int soff) {
+    const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    return static_cast<uint64_t>(t[0]) | (static_cast<uint64_t>(t[1]) << 32);
+}
+
+// Inputs x[64 a + i2] of the column (a < 32): the whole of a zero-tailed
+// row's nonzero part, which the kernel loads one row ahead.
+__device__ __forceinline__ void load_cols_u64(const __amdgpu_buffer_rsrc_t& xr, int lane, uint64_t* x0) {
+#pragma unroll
+    for (int a = 0; a < 32; ++a) x0[a] = load_u64(xr, lane * 8, (N2 * a) * 8);
+}
+
+// Phase A of one row for coset C: x0[a] = x[64 a + i2] (prefetched), the
+// column's only nonzero inputs.
+__device__ __forceinline__ void phase_a_u64(const uint64_t* x0, const __amdgpu_buffer_rsrc_t& gr, int lane, int C,
+                                           uint64_t* Y) {
+    uint64_t v[K];
+    const bool odd = C & 1, hi = C & 2;
+    gl::static_for<0, 32>([&](auto aa) {
+        constexpr int a = decltype(aa)::value;
+        // w128^(a C) = w128^(a (C & 1)) w64^(a (C >> 1))
+        uint64_t z = x0[a];
+        if (odd) z = mul_w128<a>(z);
+        if (hi) z = gl::mul_pow2<gl::E_W64 * a>(z);
+        v[gl::bitrev_c(a, 5)] = z;
+    });
+    gl::dit_pow2<5, gl::E_W32>(v);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const int j1 = C + 4 * j;
+        const auto t = __builtin_amdgcn_raw_buffer_load_b64(gr, lane * 8, (j1 * N2) * 8, 0);
+        const uint64_t w = static_cast<uint64_t>(t[0]) | (static_cast<uint64_t>(t[1]) << 32);
+        Y[j1 * PITCH + lane] = gl::mul32x4(v[j], w);
+    }
+}
+
+// One workgroup of 4 waves walks rows blockIdx.x, + gridDim.x, ...; wave S
+// takes coset (S + row step) mod 4 in phase A, so every wave takes each
+// coset's share in turn, and phase B's rows and parity as the i16 encode.
+__global__ __launch_bounds__(THREADS, 2) void ntt13_u64(const uint64_t* __restrict__ in, size_t stride, size_t len,
+                                                       size_t rows, const uint64_t* __restrict__ grid,
+                                                       uint64_t* __restrict__ out) {
+    extern __shared__ uint64_t Y[];
+    const int lane = threadIdx.x & 63;
+    const int S = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int j1b = (S >> 1) * 64 + lane;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint64_t*>(grid), static_cast<short>(0), static_cast<int>(GRID_BYTES), 0x00020000);
+    int H = 1 - (S & 1), C = S;
+    auto rsrc = [&](size_t r) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(in + r * stride), static_cast<short>(0),
+                                                 static_cast<int>(len * sizeof(uint64_t)), 0x00020000);
+    };
+    uint64_t x0[32];
+    size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
+    load_cols_u64(rsrc(row), lane, x0);
+    for (; row < rows; row += gridDim.x) {
+        __builtin_amdgcn_s_setprio(1);
+        phase_a_u64(x0, gr, lane, C, Y);
+        // the next row's first quarter of each column, in flight through phase B
+        const size_t next = row + gridDim.x;
+        if (next < rows) load_cols_u64(rsrc(next), lane, x0);
+        __syncthreads();
+        __builtin_amdgcn_s_setprio(0);
+        phase_b(Y, j1b, H, out + row * N);
+        H ^= 1;
+        C = (C + 1) & 3;
+    }
 }
 
 // grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
@@ -239,6 +343,24 @@ int build_grid(Context* c, TwiddleSet* t) {
 }
 
 }  // namespace enc13
+
+int ntt13_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
+                   TwiddleSet* t) {
+    // Rows with nonzero inputs past 2^11 (i1 >= 32) are left to the pass
+    // engine: every lane would then read its whole column, and the four
+    // waves each the whole row (measured slower than the two passes).
+    if (n != static_cast<size_t>(enc13::N) || len > static_cast<size_t>(enc13::K * enc13::N2) || stride < len) return 1;
+    if (rows == 0) return 0;
+    if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return -1;
+    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(enc13::ntt13_u64),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(enc13::LDS_BYTES)));
+    const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
+    const unsigned blocks = static_cast<unsigned>(std::min(rows, 2 * cus));
+    hipLaunchKernelGGL(enc13::ntt13_u64, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream, in, stride,
+                       len, rows, static_cast<const uint64_t*>(t->grid), out);
+    VMX_HIP(c, hipGetLastError());
+    return 0;
+}
 
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
                     TwiddleSet* t) {

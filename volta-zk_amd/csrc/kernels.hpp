@@ -19,7 +19,7 @@ int zero_bytes(Context* c, void* dst, size_t bytes);
 // ensure_twiddles(n)'s set; the inverse needs t->inv unless t->reg is present
 // (the pass engine, n >= 2^13).
 int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
-                uint64_t* out, const TwiddleSet* t, bool inverse);
+                uint64_t* out, TwiddleSet* t, bool inverse);
 // Componentwise NTT of rows x n Fp2 (u64 pairs) with base-field twiddles.
 int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t* out, const TwiddleSet* t);
 // Fused PCS encode: messages lift(w) || pads || 0 transformed without
@@ -28,6 +28,11 @@ int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t 
                      size_t n, uint64_t* out, const TwiddleSet* t);
 // Fast path for the Ligero shapes (i16 messages with rate <= 1/2 and
 // n in [2^11, 2^14]); returns 1 when the shape is not covered.
+// Forward NTT of rows of n = 2^13 canonical u64 in one pass (encode_fast.hip):
+// row r is in[r * stride .. r * stride + len), zero beyond len.  Returns 1
+// (nothing done) for other sizes, 0 on success, -1 on error.
+int ntt13_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
+                   TwiddleSet* t);
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
                     TwiddleSet* t);
 

@@ -158,7 +158,14 @@ static RegTables reg_tables(const TwiddleSet* t) {
 }
 
 int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len, size_t rows, size_t n,
-                uint64_t* out, const TwiddleSet* t, bool inverse) {
+                uint64_t* out, TwiddleSet* t, bool inverse) {
+    // n = 2^13 forward: one pass over HBM (the pass engine's two otherwise),
+    // unless its device-built table is missing inside a coarse timing scope,
+    // where tables may not grow.
+    if (!inverse && n == 8192 && (t->grid || !c->coarse_active)) {
+        const int rc = ntt13_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
+        if (rc <= 0) return rc;
+    }
     if (t->reg) return reg_ntt(c, reg_tables(t), in, in_stride, msg_len, out, rows, ilog2(n), 1, inverse);
     const uint64_t scale = inverse ? gl::inv_host(gl::canon(n)) : 1;
     const uint64_t* tw = inverse ? t->inv : t->fwd;
