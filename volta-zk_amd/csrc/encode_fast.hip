@@ -41,8 +41,10 @@ constexpr int PITCH = 65;  // u64 per LDS row of Y
 constexpr int THREADS = 256;
 constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 constexpr size_t GRID_BYTES = size_t{N1} * N2 * sizeof(uint64_t);
-// The twiddle grid, then phase A's A fragments, then its accumulator init words.
-constexpr size_t TABLE_BYTES = GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int);
+// The twiddle grid, then phase A's A fragments, then its accumulator init
+// words, then w128^k for k < 128 (the u64 rows' pre-twiddles).
+constexpr size_t W128_OFF = GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int);
+constexpr size_t TABLE_BYTES = W128_OFF + 128 * sizeof(uint64_t);
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -224,24 +226,8 @@ __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __rest
 // 128-point column DFTs run on the VALU, one coset of outputs j1 = C + 4 j'
 // per wave and one column i2 per lane:
 //   X[C + 4 j'][i2] = sum_{a < 32} w32^(a j') (w128^(a C) x[64 a + i2]),
-// the pre-twiddle w128^(a C) (a shift for even a C, two shifts and a
-// subtract for odd: w128 = 2^43 - 2^91), one 32-point shift-only DFT over a,
-// then the twiddle w^(i2 j1) into Y.  Phase B is the encode's.  The four
-// cosets share one code path (uniform branches on the coset's two bits,
-// w128^(a C) = w128^(a (C & 1)) w64^(a (C >> 1))), which keeps the kernel
-// within the instruction cache.
-
-// x w128^K for canonical x (any K >= 0).
-template <int K>
-__device__ __forceinline__ uint64_t mul_w128(uint64_t x) {
-    constexpr int k = K % 128;
-    if constexpr (k % 2 == 0) {
-        return gl::mul_pow2<gl::E_W64 * (k / 2)>(x);
-    } else {
-        constexpr int c = gl::E_W64 * ((k - 1) / 2);
-        return gl::sub(gl::mul_pow2<43 + c>(x), gl::mul_pow2<91 + c>(x));
-    }
-}
+// the pre-twiddle w128^(a C), one 32-point shift-only DFT over a, then the
+// twiddle w^(i2 j1) into Y.  Phase B is the encode's.
 
 __device__ __forceinline__ uint64_t load_u64(const __amdgpu_buffer_rsrc_t& r, int voff, int soff) {
     const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
@@ -256,19 +242,21 @@ __device__ __forceinline__ void load_cols_u64(const __amdgpu_buffer_rsrc_t& xr, 
 }
 
 // Phase A of one row for coset C: x0[a] = x[64 a + i2] (prefetched), the
-// column's only nonzero inputs.
-__device__ __forceinline__ void phase_a_u64(const uint64_t* x0, const __amdgpu_buffer_rsrc_t& gr, int lane, int C,
-                                           uint64_t* Y) {
+// column's only nonzero inputs.  The pre-twiddle w128^(a C) is the same for
+// every lane: one general multiply by a word of w128t that the wave reads
+// through the scalar cache, so every coset but C = 0 costs the same and the
+// four waves reach the row's barrier together.
+__device__ __forceinline__ void phase_a_u64(const uint64_t* x0, const uint64_t* __restrict__ w128t,
+                                           const __amdgpu_buffer_rsrc_t& gr, int lane, int C, uint64_t* Y) {
     uint64_t v[K];
-    const bool odd = C & 1, hi = C & 2;
-    gl::static_for<0, 32>([&](auto aa) {
-        constexpr int a = decltype(aa)::value;
-        // w128^(a C) = w128^(a (C & 1)) w64^(a (C >> 1))
-        uint64_t z = x0[a];
-        if (odd) z = mul_w128<a>(z);
-        if (hi) z = gl::mul_pow2<gl::E_W64 * a>(z);
-        v[gl::bitrev_c(a, 5)] = z;
-    });
+    if (C == 0) {
+#pragma unroll
+        for (int a = 0; a < 32; ++a) v[gl::bitrev_c(a, 5)] = x0[a];
+    } else {
+        v[0] = x0[0];
+#pragma unroll
+        for (int a = 1; a < 32; ++a) v[gl::bitrev_c(a, 5)] = gl::mul32x4(x0[a], w128t[(a * C) & 127]);
+    }
     gl::dit_pow2<5, gl::E_W32>(v);
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
@@ -291,6 +279,7 @@ __global__ __launch_bounds__(THREADS, 2) void ntt13_u64(const uint64_t* __restri
     const int j1b = (S >> 1) * 64 + lane;
     const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint64_t*>(grid), static_cast<short>(0), static_cast<int>(GRID_BYTES), 0x00020000);
+    const uint64_t* w128t = reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(grid) + W128_OFF);
     int H = 1 - (S & 1), C = S;
     auto rsrc = [&](size_t r) {
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(in + r * stride), static_cast<short>(0),
@@ -301,7 +290,7 @@ __global__ __launch_bounds__(THREADS, 2) void ntt13_u64(const uint64_t* __restri
     load_cols_u64(rsrc(row), lane, x0);
     for (; row < rows; row += gridDim.x) {
         __builtin_amdgcn_s_setprio(1);
-        phase_a_u64(x0, gr, lane, C, Y);
+        phase_a_u64(x0, w128t, gr, lane, C, Y);
         // the next row's first quarter of each column, in flight through phase B
         const size_t next = row + gridDim.x;
         if (next < rows) load_cols_u64(rsrc(next), lane, x0);
@@ -313,9 +302,14 @@ __global__ __launch_bounds__(THREADS, 2) void ntt13_u64(const uint64_t* __restri
     }
 }
 
-// grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
+// grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)),
+// and w128^k = w^(64 k) after the phase-A tables.
 __global__ void build_grid13(const uint64_t* __restrict__ tw, uint64_t* __restrict__ grid) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < 128) {
+        uint64_t* w128 = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(grid) + W128_OFF);
+        w128[idx] = idx < 64 ? tw[64 * idx] : gl::neg(tw[64 * (idx - 64)]);
+    }
     if (idx >= N1 * N2) return;
     const int j1 = idx / N2, i2 = idx % N2;
     const int e = i2 * j1;  // < n
