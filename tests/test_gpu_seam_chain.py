@@ -279,3 +279,26 @@ def test_written_rows_transform_and_a_later_write_into_their_tail(backend, oracl
     assert (got1 == oracle.ntt_forward_batch(want_m)).all()
     want_m[rows - 1, n - 5:] = tail
     assert (got2 == oracle.ntt_forward_batch(want_m)).all()
+
+
+@pytest.mark.parametrize("policy", [0, 1])
+def test_late_row_write_is_timed_as_the_messages_kernel(policy):
+    """Rows written late (here by a read of their buffer) are the messages
+    call's kernel: PcsRows gains their kernel time but no second call, under
+    the per-primitive timing policy and under the report's wall-only counters
+    (which time nothing)."""
+    from volta_mi355x import Backend
+    rows, cols, n = 64, 2048, 8192
+    w = rand_i16(33, rows * cols)
+    with Backend(timing_policy=policy) as b:
+        dw, dp = b.upload_device(w), b.alloc_device(1, np.uint64)
+        b.synchronize()
+        b.reset_stats()
+        msgs = b.pcs_messages_device(dw, 0, dp, 0, rows, cols, 0, n)
+        b.download_device(msgs, 0, 8)  # writes the rows
+        s = b.get_stats()
+        assert s["calls"]["pcs_rows"] == 1
+        if policy == 0:
+            assert s["kernel_ns"]["pcs_rows"] > 0
+        for x in (dw, dp, msgs):
+            b.free_device(x)

@@ -259,6 +259,9 @@ struct Context {
     size_t coarse_slot = 0;
     // counters-only
     bool counter_active = false;
+    // set while a record that adds kernel time without a call is finished
+    // (the late write of deferred message rows)
+    bool uncounted = false;
     bool counter_pending = false;
     uint64_t outstanding = 0;
     std::chrono::steady_clock::time_point phase_start{};
