@@ -540,3 +540,63 @@ def test_ntt13_one_pass_host_batch_lengths(backend, oracle, msg_len):
     padded = np.zeros((rows, n), np.uint64)
     padded[:, :msg_len] = host
     assert (got == oracle.ntt_forward_batch(padded)).all()
+
+
+# ---- n = 2^15 in one pass (ntt15.hip) ------------------------------------------------
+
+
+@pytest.mark.parametrize("msg_len", [1, 7, 2048, 2049, 4095, 4096, 4097, 8191, 8192, 8193])
+def test_ntt15_one_pass_host_batch_lengths(backend, oracle, msg_len):
+    """The host batch at n = 2^15 on both sides of each of the kernel's input
+    widths (2^11, 2^12, 2^13 nonzero inputs) and just past the last, which the
+    pass engine takes."""
+    n, rows = 1 << 15, 37
+    host = rand_fp(1500 + msg_len, (rows, msg_len))
+    host[0, 0] = P - 1
+    host[1, -1] = P - 2
+    got = backend.ntt_fp_batch(host, rows, msg_len, n)
+    padded = np.zeros((rows, n), np.uint64)
+    padded[:, :msg_len] = host
+    assert (got == oracle.ntt_forward_batch(padded)).all()
+
+
+@pytest.mark.parametrize("rows", [1, 255, 256, 257, 600])
+def test_ntt15_one_pass_device_rows(backend, oracle, rows):
+    """C4's device encode (compact rows of 2^12 -> 2^15) with fewer rows than
+    workgroups, exactly as many, and more (each workgroup walks several rows,
+    loading the next one's inputs during the current one)."""
+    n, msg_len = 1 << 15, 4096
+    host = rand_fp(1600 + rows, (rows, msg_len))
+    host[0, :4] = [0, 1, P - 1, (1 << 63) + 3]
+    d = backend.upload_device(host.reshape(-1))
+    out = backend.ntt_fp_encode_device(d, rows, msg_len, n)
+    got = backend.download_device(out).reshape(rows, n)
+    backend.free_device(d)
+    backend.free_device(out)
+    want = oracle.ntt_encode_batch(host, n)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
+
+
+@pytest.mark.parametrize("rows,cols,pad", [(300, 8192, 512), (300, 8192, 0), (3, 8192, 1024), (5, 4096, 512),
+                                           (5, 4096, 0), (3, 8192, 1025), (3, 6000, 512)])
+def test_ntt15_one_pass_message_rows(backend, oracle, rows, cols, pad):
+    """lift(w) || pads || 0 -> 2^15 through the fused encode and through the
+    reference's two calls (deferred rows): the one-pass kernel for 2^12 and
+    2^13 weight columns with up to 1024 pads, the pass engine for the rest."""
+    n = 1 << 15
+    g = np.random.Generator(np.random.PCG64(rows * 7 + cols + pad))
+    w = g.integers(-(1 << 15), 1 << 15, size=rows * cols, dtype=np.int16)
+    w[:3] = [-32768, 32767, -1]
+    pads = rand_fp(cols + pad, rows * pad) if pad else np.zeros(1, np.uint64)
+    dw, dp = backend.upload_device(w), backend.upload_device(pads)
+    fused = backend.pcs_encode_device(dw, 0, dp, 0, rows, cols, pad, n)
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, pad, n)
+    chain = backend.ntt_fp_batch_device(msgs, rows, n)
+    got_f = backend.download_device(fused).reshape(rows, n)
+    got_c = backend.download_device(chain).reshape(rows, n)
+    for b in (dw, dp, fused, msgs, chain):
+        backend.free_device(b)
+    want = oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)
+    assert (got_f == want).all()
+    assert (got_c == want).all()

@@ -1,0 +1,92 @@
+"""The one-pass 2^15-point transform (volta-zk_amd/csrc/ntt15.hip), its phases
+built for the host from the same header (ntt15.hpp, in libgl64_check.so) and
+run thread by thread between the kernel's barriers, against the oracle's
+transform of the zero-tailed rows.  The emulation poisons the exchange buffer
+before every write round and checks guard words around the LDS image and its
+table after every row, so a read of a word that the round did not write, or
+a write outside the buffer, fails here on the CPU.  CPU only."""
+import ctypes
+import pathlib
+
+import numpy as np
+import pytest
+
+import oracle
+
+LIB = pathlib.Path(__file__).resolve().parent.parent / "volta-zk_amd" / "libgl64_check.so"
+N = 1 << 15
+P = 0xFFFF_FFFF_0000_0001
+
+
+@pytest.fixture(scope="module")
+def glc():
+    if not LIB.exists():
+        pytest.fail("libgl64_check.so missing: run volta-zk_amd/build.py (or __graft_entry__.build())")
+    L = ctypes.CDLL(str(LIB))
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    L.glc_ntt15_u64.restype = ctypes.c_int
+    L.glc_ntt15_u64.argtypes = [vp, vp, sz, sz, sz, sz, vp]
+    L.glc_ntt15_msg.restype = ctypes.c_int
+    L.glc_ntt15_msg.argtypes = [vp, vp, vp, sz, sz, sz, sz, vp]
+    return L
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+@pytest.fixture(scope="module")
+def fwd():
+    return np.ascontiguousarray(oracle.ntt_twiddles(N))
+
+
+def _field(rng, shape):
+    x = rng.integers(0, 1 << 63, size=shape, dtype=np.uint64) * np.uint64(2)
+    x += rng.integers(0, 2, size=shape, dtype=np.uint64)
+    return np.where(x >= np.uint64(P), x - np.uint64(P), x)
+
+
+@pytest.mark.parametrize("length,stride", [(1, 1), (2048, 2048), (3000, 3001), (4096, 4096), (4097, 5000),
+                                           (8192, 8192)])
+def test_u64_rows_match_the_oracle(glc, fwd, length, stride):
+    rng = np.random.default_rng(length)
+    rows, blocks = 3, 2  # block 0 takes rows 0 and 2: the row loop and its prefetch run
+    src = _field(rng, (rows, stride))
+    want = np.zeros((rows, N), dtype=np.uint64)
+    want[:, :length] = src[:, :length]
+    want = oracle.ntt_forward_batch(want)
+    got = np.zeros((rows, N), dtype=np.uint64)
+    rc = glc.glc_ntt15_u64(_p(fwd), _p(src), stride, length, rows, blocks, _p(got))
+    assert rc == 0
+    assert (got == want).all()
+
+
+def test_u64_rows_edge_values(glc, fwd):
+    vals = np.array([0, 1, P - 1, P - 2, 0xFFFFFFFF, 1 << 32, (1 << 63), P - (1 << 32)], dtype=np.uint64)
+    src = np.resize(vals, (2, 4096)).astype(np.uint64)
+    want = np.zeros((2, N), dtype=np.uint64)
+    want[:, :4096] = src
+    got = np.zeros((2, N), dtype=np.uint64)
+    assert glc.glc_ntt15_u64(_p(fwd), _p(src), 4096, 4096, 2, 1, _p(got)) == 0
+    assert (got == oracle.ntt_forward_batch(want)).all()
+
+
+def test_u64_rows_refused_past_2_13(glc, fwd):
+    src = np.zeros((1, 8193), dtype=np.uint64)
+    got = np.zeros((1, N), dtype=np.uint64)
+    assert glc.glc_ntt15_u64(_p(fwd), _p(src), 8193, 8193, 1, 1, _p(got)) == 1
+
+
+@pytest.mark.parametrize("cols,pad", [(8192, 0), (8192, 512), (8192, 1024), (4096, 0), (4096, 512)])
+def test_message_rows_match_the_oracle(glc, fwd, cols, pad):
+    rng = np.random.default_rng(cols + pad)
+    rows, blocks = 3, 2
+    w = rng.integers(-32768, 32768, size=(rows, cols), dtype=np.int16)
+    w[0, :4] = [-32768, 32767, -1, 0]
+    pads = _field(rng, (rows, max(pad, 1)))
+    msgs = oracle.pcs_messages(w.reshape(-1), pads.reshape(-1) if pad else None, rows, cols, pad, N)
+    want = oracle.ntt_forward_batch(msgs.reshape(rows, N))
+    got = np.zeros((rows, N), dtype=np.uint64)
+    rc = glc.glc_ntt15_msg(_p(fwd), _p(w), _p(pads), cols, pad, rows, blocks, _p(got))
+    assert rc == 0
+    assert (got == want).all()

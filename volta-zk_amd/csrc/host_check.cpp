@@ -3,12 +3,15 @@
 // Not part of the product library.
 #include <stdint.h>
 
+#include <algorithm>
 #include <array>
 #include <utility>
+#include <vector>
 
 #include "enc13_mfma.hpp"
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
+#include "ntt15.hpp"
 
 namespace {
 using Fn = uint64_t (*)(uint64_t);
@@ -98,4 +101,110 @@ extern "C" __attribute__((visibility("default"))) void glc_enc13_phase_a(const u
                 const uint64_t g = e < 4096 ? tw_half[e] : gl::neg(tw_half[e - 4096]);
                 Y[j1 * 64 + i2] = gl::mul32x4(enc13m::recombine(acc, acc + 4), g);
             }
+}
+
+// ---- the one-pass 2^15 transform (ntt15.hip), emulated on the host ----------
+// Each workgroup's 1024 threads run the kernel's phases one after the other,
+// thread by thread, between the kernel's barriers; the exchange buffer is
+// poisoned before every write round, so a read of a word the round did not
+// write shows up in the result, and guard words around the LDS image and its
+// T2 table are checked after every row.  Returns 0, or -1 when a guard or
+// T2 changed.
+namespace {
+template <int NZ, class Src>
+int n15_emulate(const uint64_t* fwd, const Src& src, size_t rows, size_t blocks, uint64_t* out) {
+    using namespace vmx::n15;
+    constexpr int GUARD = 64;
+    constexpr uint64_t POISON = 0xA5A5A5A55A5A5A5Aull;
+    std::vector<uint64_t> tab(T1_WORDS + 1024);
+    for (int i = 0; i < T1_WORDS + 1024; ++i) tab[i] = table_word(fwd, i);
+    const Table1 t1(tab.data());
+    std::vector<uint64_t> image(LDS_WORDS + 2 * GUARD, POISON);
+    uint64_t* lds = image.data() + GUARD;
+    std::vector<std::array<uint64_t, 32>> v(THREADS);
+    std::vector<std::array<typename Src::Raw, NZ>> raw(THREADS);
+    auto intact = [&]() {
+        for (int i = 0; i < GUARD; ++i)
+            if (image[i] != POISON || image[GUARD + LDS_WORDS + i] != POISON) return false;
+        for (int t = 0; t < THREADS; ++t)
+            if (lds[T2_OFF + t] != tab[T1_WORDS + t]) return false;
+        return true;
+    };
+    auto poison = [&]() { std::fill(lds, lds + XBUF_WORDS, POISON); };
+    for (size_t b = 0; b < blocks; ++b) {
+        for (int t = 0; t < THREADS; ++t) lds[T2_OFF + t] = tab[T1_WORDS + t];
+        size_t row = b;
+        if (row < rows)
+            for (int t = 0; t < THREADS; ++t) fetch_row<NZ>(src, row, role(t).m, raw[t].data());
+        for (; row < rows; row += blocks) {
+            for (int t = 0; t < THREADS; ++t) stage_a<NZ>(v[t].data(), src, raw[t].data());
+            for (int rd = 0; rd < 2; ++rd) {
+                poison();
+                for (int t = 0; t < THREADS; ++t) {
+                    const Role r = role(t);
+                    const int h = ((t >> 6) & 1) ^ rd;
+                    uint64_t tw[16];
+                    load_tw1(tw, t1, h, r.m);
+                    if (h == 0) x1_write<0>(lds, v[t].data(), tw, r.m);
+                    else x1_write<1>(lds, v[t].data(), tw, r.m);
+                }
+                for (int t = 0; t < THREADS; ++t) {
+                    const Role r = role(t);
+                    if ((((t >> 6) & 1) ^ rd) == 0) x1_read<0>(lds, v[t].data(), r.j1b, r.k3b);
+                    else x1_read<1>(lds, v[t].data(), r.j1b, r.k3b);
+                }
+            }
+            for (int t = 0; t < THREADS; ++t) gl::dit_pow2<5, gl::E_W32>(v[t].data());
+            for (int rd = 0; rd < 2; ++rd) {
+                poison();
+                for (int t = 0; t < THREADS; ++t) {
+                    const Role r = role(t);
+                    if ((((t >> 7) & 1) ^ rd) == 0) x2_write<0>(lds, v[t].data(), r.j1b, r.k3b);
+                    else x2_write<1>(lds, v[t].data(), r.j1b, r.k3b);
+                }
+                for (int t = 0; t < THREADS; ++t) {
+                    const Role r = role(t);
+                    if ((((t >> 7) & 1) ^ rd) == 0) x2_read<0>(lds, v[t].data(), r.k3c, r.k2c);
+                    else x2_read<1>(lds, v[t].data(), r.k3c, r.k2c);
+                }
+            }
+            for (int t = 0; t < THREADS; ++t) {
+                if (row + blocks < rows) fetch_row<NZ>(src, row + blocks, role(t).m, raw[t].data());
+                gl::dit_pow2<5, gl::E_W32>(v[t].data());
+                const Role r = role(t);
+                for (int k1 = 0; k1 < 32; ++k1) out[row * N + r.k3c + 32 * r.k2c + 1024 * k1] = v[t][k1];
+            }
+            if (!intact()) return -1;
+        }
+    }
+    return 0;
+}
+}  // namespace
+
+// The kernel's choice of NZ for u64 rows (ntt15_u64_rows), then the emulation.
+extern "C" __attribute__((visibility("default"))) int glc_ntt15_u64(const uint64_t* fwd, const uint64_t* in,
+                                                                    size_t stride, size_t len, size_t rows,
+                                                                    size_t blocks, uint64_t* out) {
+    const vmx::n15::SrcU64 s{in, stride, len};
+    if (len == 0 || stride < len) return 1;
+    if (len <= 2048) return n15_emulate<2>(fwd, s, rows, blocks, out);
+    if (len <= 4096) return n15_emulate<4>(fwd, s, rows, blocks, out);
+    if (len <= 8192) return n15_emulate<8>(fwd, s, rows, blocks, out);
+    return 1;
+}
+
+// The same for message rows lift(w) || pads || 0 (ntt15_msg_rows).
+extern "C" __attribute__((visibility("default"))) int glc_ntt15_msg(const uint64_t* fwd, const int16_t* w,
+                                                                    const uint64_t* pads, size_t cols, size_t pad,
+                                                                    size_t rows, size_t blocks, uint64_t* out) {
+    const uint64_t* pp = pad ? pads : fwd;
+    if (cols == 8192 && pad <= 1024) {
+        const vmx::n15::SrcMsg<8> s{w, pp, cols, pad};
+        return pad == 0 ? n15_emulate<8>(fwd, s, rows, blocks, out) : n15_emulate<9>(fwd, s, rows, blocks, out);
+    }
+    if (cols == 4096 && pad <= 1024) {
+        const vmx::n15::SrcMsg<4> s{w, pp, cols, pad};
+        return pad == 0 ? n15_emulate<4>(fwd, s, rows, blocks, out) : n15_emulate<5>(fwd, s, rows, blocks, out);
+    }
+    return 1;
 }

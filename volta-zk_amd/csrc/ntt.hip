@@ -166,6 +166,11 @@ int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len
         const int rc = ntt13_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
         if (rc <= 0) return rc;
     }
+    // n = 2^15 forward with at most 2^13 nonzero inputs: one pass as well.
+    if (!inverse && n == 32768) {
+        const int rc = ntt15_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
+        if (rc <= 0) return rc;
+    }
     if (t->reg) return reg_ntt(c, reg_tables(t), in, in_stride, msg_len, out, rows, ilog2(n), 1, inverse);
     const uint64_t scale = inverse ? gl::inv_host(gl::canon(n)) : 1;
     const uint64_t* tw = inverse ? t->inv : t->fwd;
@@ -181,7 +186,11 @@ int ntt_fp2_rows(Context* c, const uint64_t* in, size_t rows, size_t n, uint64_t
 }
 
 int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
-                     size_t n, uint64_t* out, const TwiddleSet* t) {
+                     size_t n, uint64_t* out, TwiddleSet* t) {
+    if (n == 32768) {
+        const int rc = ntt15_msg_rows(c, w, pads, cols, pad, rows, n, out, t);
+        if (rc <= 0) return rc;
+    }
     if (t->reg) return reg_ntt_msg_i16(c, reg_tables(t), w, pads, cols, pad, out, rows, ilog2(n));
     return run_ntt(c, LoadMsgI16{w, pads, cols, pad}, StoreU64{out}, rows, n, t->fwd, 1);
 }
