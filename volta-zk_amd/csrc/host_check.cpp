@@ -143,10 +143,10 @@ int n15_emulate(const uint64_t* fwd, const Src& src, size_t rows, size_t blocks,
                 for (int t = 0; t < THREADS; ++t) {
                     const Role r = role(t);
                     const int h = ((t >> 6) & 1) ^ rd;
-                    uint64_t tw[16];
-                    load_tw1(tw, t1, h, r.m);
-                    if (h == 0) x1_write<0>(lds, v[t].data(), tw, r.m);
-                    else x1_write<1>(lds, v[t].data(), tw, r.m);
+                    uint64_t tw[8];
+                    load_tw1<0>(tw, t1, h, r.m);
+                    if (h == 0) x1_write<0>(lds, v[t].data(), tw, t1, r.m);
+                    else x1_write<1>(lds, v[t].data(), tw, t1, r.m);
                 }
                 for (int t = 0; t < THREADS; ++t) {
                     const Role r = role(t);

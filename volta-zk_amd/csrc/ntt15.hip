@@ -35,55 +35,77 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
     const int w0 = w & 1, w1 = (w >> 1) & 1;
     lds[T2_OFF + t] = tab[T1_WORDS + t];
     const Table1 t1(tab);
-    const uint32_t ooff = static_cast<uint32_t>(r.k3c + 32 * r.k2c) * 8u;
     typename Src::Raw raw[NZ];
     size_t row = blockIdx.x;
     if (row < rows) fetch_row<NZ>(src, row, r.m, raw);
     __syncthreads();
     for (; row < rows; row += gridDim.x) {
-        // The role indices pass through an opaque copy each row, so the LDS
-        // addresses derived from them are formed inside the loop (an add
-        // each) rather than hoisted out of it and kept live (which spills).
-        Role q = r;
-        uint32_t qo = ooff;
-        asm volatile("" : "+v"(q.m), "+v"(q.j1b), "+v"(q.k3b), "+v"(q.k3c), "+v"(q.k2c), "+v"(qo));
-        uint64_t v[32], tw[16];
+        // The role indices are recomputed from an opaque copy of the thread
+        // index where each phase needs them (a few adds), so neither they nor
+        // the LDS addresses formed from them are hoisted out of the loop and
+        // kept live across it (which spills).
+        auto here = [&]() {
+            int tt = t;
+            asm volatile("" : "+v"(tt));
+            return role(tt);
+        };
+        uint64_t v[32], tw[8];
         // Per row: the first half's twiddles load after stage A, the second
         // half's while the first half goes through LDS, the next row's inputs
         // during stage C.  The scheduling barriers keep each group of loads
         // where it is (hoisted, they would be live beside all 32 values).
         stage_a<NZ>(v, src, raw);
         __builtin_amdgcn_sched_barrier(0);
-        load_tw1(tw, t1, w0, q.m);
-        if (w0 == 0) x1_write<0>(lds, v, tw, q.m);
-        else x1_write<1>(lds, v, tw, q.m);
+        {
+            const Role q = here();
+            load_tw1<0>(tw, t1, w0, q.m);
+            if (w0 == 0) x1_write<0>(lds, v, tw, t1, q.m);
+            else x1_write<1>(lds, v, tw, t1, q.m);
+        }
         __builtin_amdgcn_sched_barrier(0);
-        load_tw1(tw, t1, w0 ^ 1, q.m);
+        load_tw1<0>(tw, t1, w0 ^ 1, here().m);
         __syncthreads();
-        if (w0 == 0) x1_read<0>(lds, v, q.j1b, q.k3b);
-        else x1_read<1>(lds, v, q.j1b, q.k3b);
+        {
+            const Role q = here();
+            if (w0 == 0) x1_read<0>(lds, v, q.j1b, q.k3b);
+            else x1_read<1>(lds, v, q.j1b, q.k3b);
+        }
         __syncthreads();
-        if (w0 == 1) x1_write<0>(lds, v, tw, q.m);
-        else x1_write<1>(lds, v, tw, q.m);
+        {
+            const Role q = here();
+            if (w0 == 1) x1_write<0>(lds, v, tw, t1, q.m);
+            else x1_write<1>(lds, v, tw, t1, q.m);
+        }
         __syncthreads();
-        if (w0 == 1) x1_read<0>(lds, v, q.j1b, q.k3b);
-        else x1_read<1>(lds, v, q.j1b, q.k3b);
+        {
+            const Role q = here();
+            if (w0 == 1) x1_read<0>(lds, v, q.j1b, q.k3b);
+            else x1_read<1>(lds, v, q.j1b, q.k3b);
+        }
         __syncthreads();
         gl::dit_pow2<5, gl::E_W32>(v);
         gl::static_for<0, 2>([&](auto rr) {
             constexpr int rd = decltype(rr)::value;
-            if ((w1 ^ rd) == 0) x2_write<0>(lds, v, q.j1b, q.k3b);
-            else x2_write<1>(lds, v, q.j1b, q.k3b);
+            {
+                const Role q = here();
+                if ((w1 ^ rd) == 0) x2_write<0>(lds, v, q.j1b, q.k3b);
+                else x2_write<1>(lds, v, q.j1b, q.k3b);
+            }
             __syncthreads();
-            if ((w1 ^ rd) == 0) x2_read<0>(lds, v, q.k3c, q.k2c);
-            else x2_read<1>(lds, v, q.k3c, q.k2c);
+            {
+                const Role q = here();
+                if ((w1 ^ rd) == 0) x2_read<0>(lds, v, q.k3c, q.k2c);
+                else x2_read<1>(lds, v, q.k3c, q.k2c);
+            }
             __syncthreads();
         });
-        if (row + gridDim.x < rows) fetch_row<NZ>(src, row + gridDim.x, q.m, raw);
+        if (row + gridDim.x < rows) fetch_row<NZ>(src, row + gridDim.x, here().m, raw);
         __builtin_amdgcn_sched_barrier(0);
         gl::dit_pow2<5, gl::E_W32>(v);
         // X[k3 + 32 k2 + 1024 k1]: scalar offset k1 8 KiB, non-temporal (aux bit 1)
         const auto orow = rsrc(out + row * N, size_t{N} * 8);
+        const Role q = here();
+        const uint32_t qo = static_cast<uint32_t>(q.k3c + 32 * q.k2c) * 8u;
         gl::static_for<0, 32>([&](auto k_) {
             constexpr int k1 = decltype(k_)::value;
             const v2u d = {static_cast<uint32_t>(v[k1]), static_cast<uint32_t>(v[k1] >> 32)};

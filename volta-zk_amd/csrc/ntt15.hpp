@@ -226,23 +226,33 @@ __host__ __device__ __forceinline__ void fence_half() {
 #endif
 }
 
-// The 16 first-exchange twiddles w^(k3 m) of half h (k3 = 16 h + l), h a
-// wave-uniform value, so one code path serves both halves.
+// The first-exchange twiddles w^(k3 m), k3 = 16 h + l for l in [L0, L0 + 8),
+// of half h, a wave-uniform value, so one code path serves both halves.
+template <int L0>
 __host__ __device__ __forceinline__ void load_tw1(uint64_t* tw, const Table1& t1, int h, int m) {
-    gl::static_for<0, 16>([&](auto l_) {
+    gl::static_for<0, 8>([&](auto l_) {
         constexpr int l = decltype(l_)::value;
-        tw[l] = t1.at(16 * h + l, m);
+        tw[l] = t1.at(16 * h + L0 + l, m);
     });
 }
 
 // First exchange, half H = j2b0 ^ r of a thread in role m: A[16 H + l] times
-// tw[l] = w^(k3 m) to word (l, j2, j1).
+// w^(k3 m) to word (l, j2, j1).  tw holds the twiddles of l < 8 on entry; the
+// other eight load while the first eight are written, so at most eight are
+// held at a time beside the 32 values.
 template <int H>
-__host__ __device__ __forceinline__ void x1_write(uint64_t* lds, const uint64_t* v, const uint64_t* tw, int m) {
+__host__ __device__ __forceinline__ void x1_write(uint64_t* lds, const uint64_t* v, uint64_t* tw, const Table1& t1,
+                                                  int m) {
     fence_half<H>();
     gl::static_for<0, 16>([&](auto l_) {
         constexpr int l = decltype(l_)::value, k3 = 16 * H + l;
-        lds[l * X1_PITCH + m] = k3 ? gl::mul32x4(v[k3], tw[l]) : v[k3];
+        if constexpr (l == 8) {
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_sched_barrier(0);
+#endif
+            load_tw1<8>(tw, t1, H, m);
+        }
+        lds[l * X1_PITCH + m] = k3 ? gl::mul32x4(v[k3], tw[l & 7]) : v[k3];
     });
     fence_half<H>();
 }
