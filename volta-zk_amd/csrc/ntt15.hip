@@ -45,7 +45,10 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
         // the LDS addresses formed from them are hoisted out of the loop and
         // kept live across it (which spills).
         auto here = [&]() {
-            int tt = t;
+            // the lane from mbcnt and the wave from its scalar: no register
+            // holds the thread index across the loop
+            const int lane = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+            int tt = (w << 6) + lane;
             asm volatile("" : "+v"(tt));
             return role(tt);
         };
