@@ -90,3 +90,31 @@ def test_message_rows_match_the_oracle(glc, fwd, cols, pad):
     rc = glc.glc_ntt15_msg(_p(fwd), _p(w), _p(pads), cols, pad, rows, blocks, _p(got))
     assert rc == 0
     assert (got == want).all()
+
+
+# ---- the dense one-pass 2^13 transform (ntt13r.hpp) ---------------------------------
+
+N13 = 1 << 13
+
+
+@pytest.fixture(scope="module")
+def fwd13():
+    return np.ascontiguousarray(oracle.ntt_twiddles(N13))
+
+
+@pytest.mark.parametrize("length,stride", [(1, 1), (2048, 2048), (2049, 2100), (4096, 4096), (5000, 5000),
+                                           (8192, 8192)])
+def test_ntt13_dense_rows_match_the_oracle(glc, fwd13, length, stride):
+    glc.glc_ntt13r_u64.restype = ctypes.c_int
+    glc.glc_ntt13r_u64.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_size_t] * 4 + [ctypes.c_void_p]
+    rng = np.random.default_rng(length + 13)
+    rows, blocks = 5, 2
+    src = _field(rng, (rows, stride))
+    edge = np.array([0, 1, P - 1, P - 2], dtype=np.uint64)[:stride]
+    src[0, :edge.size] = edge
+    want = np.zeros((rows, N13), dtype=np.uint64)
+    want[:, :length] = src[:, :length]
+    want = oracle.ntt_forward_batch(want)
+    got = np.zeros((rows, N13), dtype=np.uint64)
+    assert glc.glc_ntt13r_u64(_p(fwd13), _p(src), stride, length, rows, blocks, _p(got)) == 0
+    assert (got == want).all()

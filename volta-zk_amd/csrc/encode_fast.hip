@@ -27,6 +27,7 @@
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
 #include "kernels.hpp"
+#include "ntt13r.hpp"
 
 namespace vmx {
 
@@ -42,9 +43,11 @@ constexpr int THREADS = 256;
 constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 constexpr size_t GRID_BYTES = size_t{N1} * N2 * sizeof(uint64_t);
 // The twiddle grid, then phase A's A fragments, then its accumulator init
-// words, then w128^k for k < 128 (the u64 rows' pre-twiddles).
-constexpr size_t W128_OFF = GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int);
-constexpr size_t TABLE_BYTES = W128_OFF + 128 * sizeof(uint64_t);
+// words, then (256-byte aligned) the tables of the one-pass u64 transform
+// (ntt13r.hpp).
+constexpr size_t R13_OFF =
+    (GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int) + 255) & ~size_t{255};
+constexpr size_t TABLE_BYTES = R13_OFF + size_t{n13r::TABLE_WORDS} * sizeof(uint64_t);
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -218,98 +221,9 @@ __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __rest
                 keps);
 }
 
-// ---- zero-tailed u64 rows: the same split with phase A on the VALU -------------------
-// Forward NTT of rows of n = 2^13 canonical elements that are zero from
-// element 2^11 on, in one pass: the compact rows of the host batch
-// (msg_len <= 2048) and message rows the library wrote itself, whose zero
-// tail it knows.  With the inputs x[64 a + i2] (a < 32) nonzero, phase A's
-// 128-point column DFTs run on the VALU, one coset of outputs j1 = C + 4 j'
-// per wave and one column i2 per lane:
-//   X[C + 4 j'][i2] = sum_{a < 32} w32^(a j') (w128^(a C) x[64 a + i2]),
-// the pre-twiddle w128^(a C), one 32-point shift-only DFT over a, then the
-// twiddle w^(i2 j1) into Y.  Phase B is the encode's.
-
-__device__ __forceinline__ uint64_t load_u64(const __amdgpu_buffer_rsrc_t& r, int voff, int soff) {
-    const auto t = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
-    return static_cast<uint64_t>(t[0]) | (static_cast<uint64_t>(t[1]) << 32);
-}
-
-// Inputs x[64 a + i2] of the column (a < 32): the whole of a zero-tailed
-// row's nonzero part, which the kernel loads one row ahead.
-__device__ __forceinline__ void load_cols_u64(const __amdgpu_buffer_rsrc_t& xr, int lane, uint64_t* x0) {
-#pragma unroll
-    for (int a = 0; a < 32; ++a) x0[a] = load_u64(xr, lane * 8, (N2 * a) * 8);
-}
-
-// Phase A of one row for coset C: x0[a] = x[64 a + i2] (prefetched), the
-// column's only nonzero inputs.  The pre-twiddle w128^(a C) is the same for
-// every lane: one general multiply by a word of w128t that the wave reads
-// through the scalar cache, so every coset but C = 0 costs the same and the
-// four waves reach the row's barrier together.
-__device__ __forceinline__ void phase_a_u64(const uint64_t* x0, const uint64_t* __restrict__ w128t,
-                                           const __amdgpu_buffer_rsrc_t& gr, int lane, int C, uint64_t* Y) {
-    uint64_t v[K];
-    if (C == 0) {
-#pragma unroll
-        for (int a = 0; a < 32; ++a) v[gl::bitrev_c(a, 5)] = x0[a];
-    } else {
-        v[0] = x0[0];
-#pragma unroll
-        for (int a = 1; a < 32; ++a) v[gl::bitrev_c(a, 5)] = gl::mul32x4(x0[a], w128t[(a * C) & 127]);
-    }
-    gl::dit_pow2<5, gl::E_W32>(v);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) {
-        const int j1 = C + 4 * j;
-        const auto t = __builtin_amdgcn_raw_buffer_load_b64(gr, lane * 8, (j1 * N2) * 8, 0);
-        const uint64_t w = static_cast<uint64_t>(t[0]) | (static_cast<uint64_t>(t[1]) << 32);
-        Y[j1 * PITCH + lane] = gl::mul32x4(v[j], w);
-    }
-}
-
-// One workgroup of 4 waves walks rows blockIdx.x, + gridDim.x, ...; wave S
-// takes coset (S + row step) mod 4 in phase A, so every wave takes each
-// coset's share in turn, and phase B's rows and parity as the i16 encode.
-__global__ __launch_bounds__(THREADS, 2) void ntt13_u64(const uint64_t* __restrict__ in, size_t stride, size_t len,
-                                                       size_t rows, const uint64_t* __restrict__ grid,
-                                                       uint64_t* __restrict__ out) {
-    extern __shared__ uint64_t Y[];
-    const int lane = threadIdx.x & 63;
-    const int S = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int j1b = (S >> 1) * 64 + lane;
-    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint64_t*>(grid), static_cast<short>(0), static_cast<int>(GRID_BYTES), 0x00020000);
-    const uint64_t* w128t = reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(grid) + W128_OFF);
-    int H = 1 - (S & 1), C = S;
-    auto rsrc = [&](size_t r) {
-        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(in + r * stride), static_cast<short>(0),
-                                                 static_cast<int>(len * sizeof(uint64_t)), 0x00020000);
-    };
-    uint64_t x0[32];
-    size_t row = blockIdx.x;  // < rows: the grid never exceeds the row count
-    load_cols_u64(rsrc(row), lane, x0);
-    for (; row < rows; row += gridDim.x) {
-        __builtin_amdgcn_s_setprio(1);
-        phase_a_u64(x0, w128t, gr, lane, C, Y);
-        // the next row's first quarter of each column, in flight through phase B
-        const size_t next = row + gridDim.x;
-        if (next < rows) load_cols_u64(rsrc(next), lane, x0);
-        __syncthreads();
-        __builtin_amdgcn_s_setprio(0);
-        phase_b(Y, j1b, H, out + row * N);
-        H ^= 1;
-        C = (C + 1) & 3;
-    }
-}
-
-// grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)),
-// and w128^k = w^(64 k) after the phase-A tables.
+// grid[j1 * 64 + i2] = w^(i2 j1) from the half table (w^e = -w^(e - n/2)).
 __global__ void build_grid13(const uint64_t* __restrict__ tw, uint64_t* __restrict__ grid) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx < 128) {
-        uint64_t* w128 = reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(grid) + W128_OFF);
-        w128[idx] = idx < 64 ? tw[64 * idx] : gl::neg(tw[64 * (idx - 64)]);
-    }
     if (idx >= N1 * N2) return;
     const int j1 = idx / N2, i2 = idx % N2;
     const int e = i2 * j1;  // < n
@@ -324,6 +238,101 @@ __global__ void build_phase_a13(const uint64_t* __restrict__ tw, int8_t* __restr
     if (idx < static_cast<int>(enc13m::INIT_WORDS)) init[idx] = enc13m::init_word(tw, idx >> 3, idx & 7);
 }
 
+// The dense transform's T1 and T2 (ntt13r.hpp) after the encode's tables.
+__global__ void build_r13(const uint64_t* __restrict__ tw, uint64_t* __restrict__ tab) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx < n13r::TABLE_WORDS) tab[idx] = n13r::table_word(tw, idx);
+}
+
+// One-pass transform of 2^13-point u64 rows that may be nonzero up to element
+// 256 NZ (ntt13r.hpp): persistent workgroups of 256 threads, four per CU,
+// one row each at a time, no prefetch (the other workgroups on the CU run
+// while one waits on its row's loads).
+template <int NZ>
+__global__ __launch_bounds__(n13r::THREADS, 4) void ntt13r_rows(const uint64_t* __restrict__ in, size_t stride,
+                                                                size_t len, size_t rows,
+                                                                const uint64_t* __restrict__ tab,
+                                                                uint64_t* __restrict__ out) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    using namespace n13r;
+    extern __shared__ uint64_t lds[];
+    const int t = static_cast<int>(threadIdx.x);
+    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int w0 = w & 1, w1 = w >> 1;
+    lds[T2_OFF + t] = tab[T1_WORDS + t];
+    const Table1 t1(tab);
+    __syncthreads();
+    // role indices recomputed per phase from mbcnt (nothing kept live across the loop)
+    auto here = [&]() {
+        const int lane = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+        int tt = (w << 6) + lane;
+        asm volatile("" : "+v"(tt));
+        return role(tt);
+    };
+    for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        uint64_t v[32], tw[8];
+        load_row<NZ>(v, in, stride, len, row, here().m);
+        gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v);
+        __builtin_amdgcn_sched_barrier(0);
+        {
+            const Role q = here();
+            load_tw1<0>(tw, t1, w0, q.m);
+            if (w0 == 0) x1_write<0>(lds, v, tw, t1, q.m);
+            else x1_write<1>(lds, v, tw, t1, q.m);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_tw1<0>(tw, t1, w0 ^ 1, here().m);
+        __syncthreads();
+        {
+            const Role q = here();
+            if (w0 == 0) x1_read<0>(lds, v, q.j1b, q.k3b);
+            else x1_read<1>(lds, v, q.j1b, q.k3b);
+        }
+        __syncthreads();
+        {
+            const Role q = here();
+            if (w0 == 1) x1_write<0>(lds, v, tw, t1, q.m);
+            else x1_write<1>(lds, v, tw, t1, q.m);
+        }
+        __syncthreads();
+        {
+            const Role q = here();
+            if (w0 == 1) x1_read<0>(lds, v, q.j1b, q.k3b);
+            else x1_read<1>(lds, v, q.j1b, q.k3b);
+        }
+        __syncthreads();
+        gl::dit_pow2<5, gl::E_W32>(v);
+        gl::static_for<0, 2>([&](auto rr) {
+            constexpr int rd = decltype(rr)::value;
+            {
+                const Role q = here();
+                if ((w1 ^ rd) == 0) x2_write<0>(lds, v, q.j1b, q.k3b);
+                else x2_write<1>(lds, v, q.j1b, q.k3b);
+            }
+            __syncthreads();
+            {
+                const Role q = here();
+                if ((w1 ^ rd) == 0) x2_read<0>(lds, v, q.k3c, q.xc);
+                else x2_read<1>(lds, v, q.k3c, q.xc);
+            }
+            __syncthreads();
+        });
+        stage_c(v);
+        // X[k3 + 32 (p + 4 x) + 1024 k1] from slot p + 4 k1: lane offset (k3 + 128 x) 8,
+        // scalar offset (32 p + 1024 k1) 8, non-temporal (aux bit 1)
+        const auto orow = rsrc(out + row * N, size_t{N} * 8);
+        const Role q = here();
+        const uint32_t qo = static_cast<uint32_t>(q.k3c + 128 * q.xc) * 8u;
+        gl::static_for<0, 32>([&](auto s_) {
+            constexpr int s = decltype(s_)::value, pp = s & 3, k1 = s >> 2;
+            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+            const v2u d = {static_cast<uint32_t>(v[s]), static_cast<uint32_t>(v[s] >> 32)};
+            __builtin_amdgcn_raw_buffer_store_b64(d, orow, qo, (32 * pp + 1024 * k1) * 8u, 2);
+        });
+    }
+#endif
+}
+
 int build_grid(Context* c, TwiddleSet* t) {
     hipLaunchKernelGGL(build_grid13, dim3((N1 * N2 + 255) / 256), dim3(256), 0, c->stream,
                        static_cast<const uint64_t*>(t->fwd), t->grid);
@@ -333,25 +342,28 @@ int build_grid(Context* c, TwiddleSet* t) {
     hipLaunchKernelGGL(build_phase_a13, dim3(static_cast<unsigned>((enc13m::FRAG_BYTES / 16 + 255) / 256)), dim3(256),
                        0, c->stream, static_cast<const uint64_t*>(t->fwd), frags, init);
     VMX_HIP(c, hipGetLastError());
+    hipLaunchKernelGGL(build_r13, dim3((n13r::TABLE_WORDS + 255) / 256), dim3(256), 0, c->stream,
+                       static_cast<const uint64_t*>(t->fwd),
+                       reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(t->grid) + R13_OFF));
+    VMX_HIP(c, hipGetLastError());
     return 0;
 }
 
 }  // namespace enc13
 
-int ntt13_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
-                   TwiddleSet* t) {
-    // Rows with nonzero inputs past 2^11 (i1 >= 32) are left to the pass
-    // engine: every lane would then read its whole column, and the four
-    // waves each the whole row (measured slower than the two passes).
-    if (n != static_cast<size_t>(enc13::N) || len > static_cast<size_t>(enc13::K * enc13::N2) || stride < len) return 1;
+int ntt13r_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
+                    TwiddleSet* t) {
+    if (n != static_cast<size_t>(n13r::N) || len == 0 || len > n || stride < len || !t->fwd) return 1;
+    if (!t->grid && c->coarse_active) return 1;  // tables may not grow inside a coarse scope
     if (rows == 0) return 0;
     if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return -1;
-    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(enc13::ntt13_u64),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(enc13::LDS_BYTES)));
+    const uint64_t* tab =
+        reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(t->grid) + enc13::R13_OFF);
     const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
-    const unsigned blocks = static_cast<unsigned>(std::min(rows, 2 * cus));
-    hipLaunchKernelGGL(enc13::ntt13_u64, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream, in, stride,
-                       len, rows, static_cast<const uint64_t*>(t->grid), out);
+    const unsigned blocks = static_cast<unsigned>(std::min(rows, 4 * cus));
+    auto k = len <= 2048 ? enc13::ntt13r_rows<8> : len <= 4096 ? enc13::ntt13r_rows<16> : enc13::ntt13r_rows<32>;
+    hipLaunchKernelGGL(k, dim3(blocks), dim3(n13r::THREADS), n13r::LDS_BYTES, c->stream, in, stride, len, rows, tab,
+                       out);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }

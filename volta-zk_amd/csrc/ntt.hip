@@ -163,7 +163,7 @@ int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len
     // unless its device-built table is missing inside a coarse timing scope,
     // where tables may not grow.
     if (!inverse && n == 8192 && (t->grid || !c->coarse_active)) {
-        const int rc = ntt13_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
+        const int rc = ntt13r_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
         if (rc <= 0) return rc;
     }
     // n = 2^15 forward with at most 2^13 nonzero inputs: one pass as well.
