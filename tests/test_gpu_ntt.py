@@ -545,11 +545,11 @@ def test_ntt13_one_pass_host_batch_lengths(backend, oracle, msg_len):
 # ---- n = 2^15 in one pass (ntt15.hip) ------------------------------------------------
 
 
-@pytest.mark.parametrize("msg_len", [1, 7, 2048, 2049, 4095, 4096, 4097, 8191, 8192, 8193])
+@pytest.mark.parametrize("msg_len", [1, 7, 2048, 2049, 4095, 4096, 4097, 8191, 8192, 8193, 16384, 16896, 32768])
 def test_ntt15_one_pass_host_batch_lengths(backend, oracle, msg_len):
     """The host batch at n = 2^15 on both sides of each of the kernel's input
-    widths (2^11, 2^12, 2^13 nonzero inputs) and just past the last, which the
-    pass engine takes."""
+    widths (2^11 .. 2^15 nonzero inputs; up to 2^13 the next row's inputs load
+    a row ahead, past it at the top of their own row)."""
     n, rows = 1 << 15, 37
     host = rand_fp(1500 + msg_len, (rows, msg_len))
     host[0, 0] = P - 1

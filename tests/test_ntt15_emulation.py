@@ -47,7 +47,7 @@ def _field(rng, shape):
 
 
 @pytest.mark.parametrize("length,stride", [(1, 1), (2048, 2048), (3000, 3001), (4096, 4096), (4097, 5000),
-                                           (8192, 8192)])
+                                           (8192, 8192), (8193, 8193), (16896, 16896), (32768, 32768)])
 def test_u64_rows_match_the_oracle(glc, fwd, length, stride):
     rng = np.random.default_rng(length)
     rows, blocks = 3, 2  # block 0 takes rows 0 and 2: the row loop and its prefetch run
@@ -71,10 +71,10 @@ def test_u64_rows_edge_values(glc, fwd):
     assert (got == oracle.ntt_forward_batch(want)).all()
 
 
-def test_u64_rows_refused_past_2_13(glc, fwd):
-    src = np.zeros((1, 8193), dtype=np.uint64)
+def test_u64_rows_refused_past_n(glc, fwd):
+    src = np.zeros((1, N + 1), dtype=np.uint64)
     got = np.zeros((1, N), dtype=np.uint64)
-    assert glc.glc_ntt15_u64(_p(fwd), _p(src), 8193, 8193, 1, 1, _p(got)) == 1
+    assert glc.glc_ntt15_u64(_p(fwd), _p(src), N + 1, N + 1, 1, 1, _p(got)) == 1
 
 
 @pytest.mark.parametrize("cols,pad", [(8192, 0), (8192, 512), (8192, 1024), (4096, 0), (4096, 512)])

@@ -191,6 +191,8 @@ extern "C" __attribute__((visibility("default"))) int glc_ntt15_u64(const uint64
     if (len <= 2048) return n15_emulate<2>(fwd, s, rows, blocks, out);
     if (len <= 4096) return n15_emulate<4>(fwd, s, rows, blocks, out);
     if (len <= 8192) return n15_emulate<8>(fwd, s, rows, blocks, out);
+    if (len <= 16384) return n15_emulate<16>(fwd, s, rows, blocks, out);
+    if (len <= 32768) return n15_emulate<32>(fwd, s, rows, blocks, out);
     return 1;
 }
 

@@ -29,7 +29,7 @@ int ntt_msg_i16_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t 
 // Fast path for the Ligero shapes (i16 messages with rate <= 1/2 and
 // n in [2^11, 2^14]); returns 1 when the shape is not covered.
 // Forward NTT of rows of n = 2^15 in one pass (ntt15.hip): u64 rows as for
-// ntt13r_u64_rows with len <= 2^13, or message rows lift(w) || pads || 0 with
+// ntt13r_u64_rows (len <= n), or message rows lift(w) || pads || 0 with
 // cols = 2^12 or 2^13 and pad <= 1024.  Returns 1 (nothing done) for other
 // shapes, 0 on success, -1 on error.
 int ntt15_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,

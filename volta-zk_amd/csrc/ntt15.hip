@@ -1,6 +1,6 @@
 // ntt15.hip -- one-pass forward NTT of 2^15 points over HBM, for rows whose
 // inputs are zero from index 1024 NZ on (the rate-1/8 and rate-1/4 Ligero
-// encodes of 2^15-point codewords).  The split and the exchanges are in
+// encodes of 2^15-point codewords, and denser rows up to all 2^15 inputs).  The split and the exchanges are in
 // ntt15.hpp.
 //
 // One workgroup of 1024 threads per CU walks the rows (persistent grid); a
@@ -35,9 +35,14 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
     const int w0 = w & 1, w1 = (w >> 1) & 1;
     lds[T2_OFF + t] = tab[T1_WORDS + t];
     const Table1 t1(tab);
+    // Up to 4 nonzero inputs per thread the next row's load a row ahead, into
+    // registers; denser rows load at the top of their own row.  Measured: C4
+    // (4 u64) 5.07 -> 5.03 ms with the prefetch, p15 (8 i16 + 1 pad) 3.92 ->
+    // 4.27 ms, whose 11 prefetch registers spill beside the 32 values.
+    constexpr bool PREFETCH = NZ <= 4;
     typename Src::Raw raw[NZ];
     size_t row = blockIdx.x;
-    if (row < rows) fetch_row<NZ>(src, row, r.m, raw);
+    if (PREFETCH && row < rows) fetch_row<NZ>(src, row, r.m, raw);
     __syncthreads();
     for (; row < rows; row += gridDim.x) {
         // The role indices are recomputed from an opaque copy of the thread
@@ -57,6 +62,7 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
         // half's while the first half goes through LDS, the next row's inputs
         // during stage C.  The scheduling barriers keep each group of loads
         // where it is (hoisted, they would be live beside all 32 values).
+        if constexpr (!PREFETCH) fetch_row<NZ>(src, row, here().m, raw);
         stage_a<NZ>(v, src, raw);
         __builtin_amdgcn_sched_barrier(0);
         {
@@ -102,7 +108,7 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
             }
             __syncthreads();
         });
-        if (row + gridDim.x < rows) fetch_row<NZ>(src, row + gridDim.x, here().m, raw);
+        if (PREFETCH && row + gridDim.x < rows) fetch_row<NZ>(src, row + gridDim.x, here().m, raw);
         __builtin_amdgcn_sched_barrier(0);
         gl::dit_pow2<5, gl::E_W32>(v);
         // X[k3 + 32 k2 + 1024 k1]: scalar offset k1 8 KiB, non-temporal (aux bit 1)
@@ -149,14 +155,15 @@ int launch(Context* c, const Src& src, size_t rows, uint64_t* out, TwiddleSet* t
 
 int ntt15_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
                    TwiddleSet* t) {
-    if (n != static_cast<size_t>(n15::N) || len == 0 || stride < len || !t->fwd) return 1;
+    if (n != static_cast<size_t>(n15::N) || len == 0 || len > n || stride < len || !t->fwd) return 1;
     if (!t->grid && c->coarse_active) return 1;  // tables may not grow inside a coarse scope
     if (rows == 0) return 0;
     const n15::SrcU64 s{in, stride, len};
     if (len <= 2048) return n15::launch<2>(c, s, rows, out, t);
     if (len <= 4096) return n15::launch<4>(c, s, rows, out, t);
     if (len <= 8192) return n15::launch<8>(c, s, rows, out, t);
-    return 1;
+    if (len <= 16384) return n15::launch<16>(c, s, rows, out, t);
+    return n15::launch<32>(c, s, rows, out, t);
 }
 
 int ntt15_msg_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t cols, size_t pad, size_t rows,
