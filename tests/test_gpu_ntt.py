@@ -600,3 +600,37 @@ def test_ntt15_one_pass_message_rows(backend, oracle, rows, cols, pad):
     want = oracle.pcs_encode_i16(w, pads, rows, cols, pad, n)
     assert (got_f == want).all()
     assert (got_c == want).all()
+
+
+# ---- n = 2^14 in one pass (ntt_rr.hip) -----------------------------------------------
+
+
+@pytest.mark.parametrize("msg_len", [1, 4096, 4097, 8192, 8193, 16384])
+def test_ntt14_one_pass_host_batch_lengths(backend, oracle, msg_len):
+    """The host batch at n = 2^14 on both sides of each stage-A input width
+    (2^12, 2^13, 2^14 nonzero inputs)."""
+    n, rows = 1 << 14, 37
+    host = rand_fp(1700 + msg_len, (rows, msg_len))
+    host[0, 0] = P - 1
+    host[1, -1] = P - 2
+    got = backend.ntt_fp_batch(host, rows, msg_len, n)
+    padded = np.zeros((rows, n), np.uint64)
+    padded[:, :msg_len] = host
+    assert (got == oracle.ntt_forward_batch(padded)).all()
+
+
+@pytest.mark.parametrize("rows", [1, 255, 256, 257, 700])
+def test_ntt14_one_pass_device_rows(backend, oracle, rows):
+    """C1's device encode (compact rows of 2^12 -> 2^14) with fewer rows than
+    workgroups, as many, and more (each workgroup walks several rows)."""
+    n, msg_len = 1 << 14, 4096
+    host = rand_fp(1800 + rows, (rows, msg_len))
+    host[0, :4] = [0, 1, P - 1, (1 << 63) + 3]
+    d = backend.upload_device(host.reshape(-1))
+    out = backend.ntt_fp_encode_device(d, rows, msg_len, n)
+    got = backend.download_device(out).reshape(rows, n)
+    backend.free_device(d)
+    backend.free_device(out)
+    want = oracle.ntt_encode_batch(host, n)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:8].tolist()} differ"

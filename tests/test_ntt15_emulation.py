@@ -92,7 +92,7 @@ def test_message_rows_match_the_oracle(glc, fwd, cols, pad):
     assert (got == want).all()
 
 
-# ---- the dense one-pass 2^13 transform (ntt13r.hpp) ---------------------------------
+# ---- the one-pass 2^13 and 2^14 transforms of rows that may be dense (ntt_rr.hpp) ---
 
 N13 = 1 << 13
 
@@ -117,4 +117,30 @@ def test_ntt13_dense_rows_match_the_oracle(glc, fwd13, length, stride):
     want = oracle.ntt_forward_batch(want)
     got = np.zeros((rows, N13), dtype=np.uint64)
     assert glc.glc_ntt13r_u64(_p(fwd13), _p(src), stride, length, rows, blocks, _p(got)) == 0
+    assert (got == want).all()
+
+
+N14 = 1 << 14
+
+
+@pytest.fixture(scope="module")
+def fwd14():
+    return np.ascontiguousarray(oracle.ntt_twiddles(N14))
+
+
+@pytest.mark.parametrize("length,stride", [(1, 1), (4096, 4096), (4097, 4100), (8192, 8192), (9000, 9000),
+                                           (16384, 16384)])
+def test_ntt14_rows_match_the_oracle(glc, fwd14, length, stride):
+    glc.glc_ntt14r_u64.restype = ctypes.c_int
+    glc.glc_ntt14r_u64.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_size_t] * 4 + [ctypes.c_void_p]
+    rng = np.random.default_rng(length + 14)
+    rows, blocks = 5, 2
+    src = _field(rng, (rows, stride))
+    edge = np.array([0, 1, P - 1, P - 2], dtype=np.uint64)[:stride]
+    src[0, :edge.size] = edge
+    want = np.zeros((rows, N14), dtype=np.uint64)
+    want[:, :length] = src[:, :length]
+    want = oracle.ntt_forward_batch(want)
+    got = np.zeros((rows, N14), dtype=np.uint64)
+    assert glc.glc_ntt14r_u64(_p(fwd14), _p(src), stride, length, rows, blocks, _p(got)) == 0
     assert (got == want).all()

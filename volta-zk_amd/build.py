@@ -22,7 +22,7 @@ BUILD = HERE / "_build"
 LIB = HERE / "libvolta_mi355x_backend.so"
 # Host build of the device arithmetic headers for the CPU tests (not shipped).
 CHECK_LIB = HERE / "libgl64_check.so"
-SOURCES = ["context.cpp", "ntt.hip", "ntt_reg.hip", "encode_fast.hip", "ntt15.hip", "pcs.hip", "merkle.hip", "x4.hip", "abi_pcs.cpp",
+SOURCES = ["context.cpp", "ntt.hip", "ntt_reg.hip", "encode_fast.hip", "ntt15.hip", "ntt_rr.hip", "pcs.hip", "merkle.hip", "x4.hip", "abi_pcs.cpp",
            "abi_stubs.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

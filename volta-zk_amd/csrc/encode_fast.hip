@@ -27,7 +27,7 @@
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
 #include "kernels.hpp"
-#include "ntt13r.hpp"
+#include "ntt_rr.hpp"
 
 namespace vmx {
 
@@ -44,10 +44,10 @@ constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 constexpr size_t GRID_BYTES = size_t{N1} * N2 * sizeof(uint64_t);
 // The twiddle grid, then phase A's A fragments, then its accumulator init
 // words, then (256-byte aligned) the tables of the one-pass u64 transform
-// (ntt13r.hpp).
+// (ntt_rr.hpp, n = 2^13).
 constexpr size_t R13_OFF =
     (GRID_BYTES + enc13m::FRAG_BYTES + enc13m::INIT_WORDS * sizeof(int) + 255) & ~size_t{255};
-constexpr size_t TABLE_BYTES = R13_OFF + size_t{n13r::TABLE_WORDS} * sizeof(uint64_t);
+constexpr size_t TABLE_BYTES = R13_OFF + size_t{rr::Shape<3>::TABLE_WORDS} * sizeof(uint64_t);
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -238,101 +238,6 @@ __global__ void build_phase_a13(const uint64_t* __restrict__ tw, int8_t* __restr
     if (idx < static_cast<int>(enc13m::INIT_WORDS)) init[idx] = enc13m::init_word(tw, idx >> 3, idx & 7);
 }
 
-// The dense transform's T1 and T2 (ntt13r.hpp) after the encode's tables.
-__global__ void build_r13(const uint64_t* __restrict__ tw, uint64_t* __restrict__ tab) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx < n13r::TABLE_WORDS) tab[idx] = n13r::table_word(tw, idx);
-}
-
-// One-pass transform of 2^13-point u64 rows that may be nonzero up to element
-// 256 NZ (ntt13r.hpp): persistent workgroups of 256 threads, four per CU,
-// one row each at a time, no prefetch (the other workgroups on the CU run
-// while one waits on its row's loads).
-template <int NZ>
-__global__ __launch_bounds__(n13r::THREADS, 4) void ntt13r_rows(const uint64_t* __restrict__ in, size_t stride,
-                                                                size_t len, size_t rows,
-                                                                const uint64_t* __restrict__ tab,
-                                                                uint64_t* __restrict__ out) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    using namespace n13r;
-    extern __shared__ uint64_t lds[];
-    const int t = static_cast<int>(threadIdx.x);
-    const int w = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int w0 = w & 1, w1 = w >> 1;
-    lds[T2_OFF + t] = tab[T1_WORDS + t];
-    const Table1 t1(tab);
-    __syncthreads();
-    // role indices recomputed per phase from mbcnt (nothing kept live across the loop)
-    auto here = [&]() {
-        const int lane = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
-        int tt = (w << 6) + lane;
-        asm volatile("" : "+v"(tt));
-        return role(tt);
-    };
-    for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
-        uint64_t v[32], tw[8];
-        load_row<NZ>(v, in, stride, len, row, here().m);
-        gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v);
-        __builtin_amdgcn_sched_barrier(0);
-        {
-            const Role q = here();
-            load_tw1<0>(tw, t1, w0, q.m);
-            if (w0 == 0) x1_write<0>(lds, v, tw, t1, q.m);
-            else x1_write<1>(lds, v, tw, t1, q.m);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        load_tw1<0>(tw, t1, w0 ^ 1, here().m);
-        __syncthreads();
-        {
-            const Role q = here();
-            if (w0 == 0) x1_read<0>(lds, v, q.j1b, q.k3b);
-            else x1_read<1>(lds, v, q.j1b, q.k3b);
-        }
-        __syncthreads();
-        {
-            const Role q = here();
-            if (w0 == 1) x1_write<0>(lds, v, tw, t1, q.m);
-            else x1_write<1>(lds, v, tw, t1, q.m);
-        }
-        __syncthreads();
-        {
-            const Role q = here();
-            if (w0 == 1) x1_read<0>(lds, v, q.j1b, q.k3b);
-            else x1_read<1>(lds, v, q.j1b, q.k3b);
-        }
-        __syncthreads();
-        gl::dit_pow2<5, gl::E_W32>(v);
-        gl::static_for<0, 2>([&](auto rr) {
-            constexpr int rd = decltype(rr)::value;
-            {
-                const Role q = here();
-                if ((w1 ^ rd) == 0) x2_write<0>(lds, v, q.j1b, q.k3b);
-                else x2_write<1>(lds, v, q.j1b, q.k3b);
-            }
-            __syncthreads();
-            {
-                const Role q = here();
-                if ((w1 ^ rd) == 0) x2_read<0>(lds, v, q.k3c, q.xc);
-                else x2_read<1>(lds, v, q.k3c, q.xc);
-            }
-            __syncthreads();
-        });
-        stage_c(v);
-        // X[k3 + 32 (p + 4 x) + 1024 k1] from slot p + 4 k1: lane offset (k3 + 128 x) 8,
-        // scalar offset (32 p + 1024 k1) 8, non-temporal (aux bit 1)
-        const auto orow = rsrc(out + row * N, size_t{N} * 8);
-        const Role q = here();
-        const uint32_t qo = static_cast<uint32_t>(q.k3c + 128 * q.xc) * 8u;
-        gl::static_for<0, 32>([&](auto s_) {
-            constexpr int s = decltype(s_)::value, pp = s & 3, k1 = s >> 2;
-            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-            const v2u d = {static_cast<uint32_t>(v[s]), static_cast<uint32_t>(v[s] >> 32)};
-            __builtin_amdgcn_raw_buffer_store_b64(d, orow, qo, (32 * pp + 1024 * k1) * 8u, 2);
-        });
-    }
-#endif
-}
-
 int build_grid(Context* c, TwiddleSet* t) {
     hipLaunchKernelGGL(build_grid13, dim3((N1 * N2 + 255) / 256), dim3(256), 0, c->stream,
                        static_cast<const uint64_t*>(t->fwd), t->grid);
@@ -342,30 +247,15 @@ int build_grid(Context* c, TwiddleSet* t) {
     hipLaunchKernelGGL(build_phase_a13, dim3(static_cast<unsigned>((enc13m::FRAG_BYTES / 16 + 255) / 256)), dim3(256),
                        0, c->stream, static_cast<const uint64_t*>(t->fwd), frags, init);
     VMX_HIP(c, hipGetLastError());
-    hipLaunchKernelGGL(build_r13, dim3((n13r::TABLE_WORDS + 255) / 256), dim3(256), 0, c->stream,
-                       static_cast<const uint64_t*>(t->fwd),
-                       reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(t->grid) + R13_OFF));
-    VMX_HIP(c, hipGetLastError());
-    return 0;
+    return build_rr13_table(c, static_cast<const uint64_t*>(t->fwd),
+                            reinterpret_cast<uint64_t*>(reinterpret_cast<unsigned char*>(t->grid) + R13_OFF));
 }
 
 }  // namespace enc13
 
-int ntt13r_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
-                    TwiddleSet* t) {
-    if (n != static_cast<size_t>(n13r::N) || len == 0 || len > n || stride < len || !t->fwd) return 1;
-    if (!t->grid && c->coarse_active) return 1;  // tables may not grow inside a coarse scope
-    if (rows == 0) return 0;
-    if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return -1;
-    const uint64_t* tab =
-        reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(t->grid) + enc13::R13_OFF);
-    const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
-    const unsigned blocks = static_cast<unsigned>(std::min(rows, 4 * cus));
-    auto k = len <= 2048 ? enc13::ntt13r_rows<8> : len <= 4096 ? enc13::ntt13r_rows<16> : enc13::ntt13r_rows<32>;
-    hipLaunchKernelGGL(k, dim3(blocks), dim3(n13r::THREADS), n13r::LDS_BYTES, c->stream, in, stride, len, rows, tab,
-                       out);
-    VMX_HIP(c, hipGetLastError());
-    return 0;
+const uint64_t* enc13_rr_table(Context* c, TwiddleSet* t) {
+    if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return nullptr;
+    return reinterpret_cast<const uint64_t*>(reinterpret_cast<const unsigned char*>(t->grid) + enc13::R13_OFF);
 }
 
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,

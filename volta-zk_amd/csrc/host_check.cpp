@@ -11,7 +11,7 @@
 #include "enc13_mfma.hpp"
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
-#include "ntt13r.hpp"
+#include "ntt_rr.hpp"
 #include "ntt15.hpp"
 
 namespace {
@@ -212,87 +212,100 @@ extern "C" __attribute__((visibility("default"))) int glc_ntt15_msg(const uint64
     return 1;
 }
 
-// ---- the dense one-pass 2^13 transform (encode_fast.hip ntt13r_rows), emulated -------
-// As for the 2^15 transform: the workgroup's 256 threads run the phases one
-// after the other between the kernel's barriers, on a poisoned exchange
-// buffer with guard words.
+// ---- the one-pass 2^13 / 2^14 transforms (ntt_rr.hip), emulated ---------------------
+// As for the 2^15 transform: the workgroup's threads run the phases one after
+// the other between the kernel's barriers, on a poisoned exchange buffer with
+// guard words.
 namespace {
-template <int NZ>
-int n13r_emulate(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t blocks,
-                 uint64_t* out) {
-    using namespace vmx::n13r;
+template <int B, int NZ>
+int rr_emulate(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t blocks,
+               uint64_t* out) {
+    using namespace vmx::rr;
+    using S = Shape<B>;
     constexpr int GUARD = 64;
     constexpr uint64_t POISON = 0xA5A5A5A55A5A5A5Aull;
-    std::vector<uint64_t> tab(TABLE_WORDS);
-    for (int i = 0; i < TABLE_WORDS; ++i) tab[i] = table_word(fwd, i);
-    const Table1 t1(tab.data());
-    std::vector<uint64_t> image(LDS_WORDS + 2 * GUARD, POISON);
+    std::vector<uint64_t> tab(S::TABLE_WORDS);
+    for (int i = 0; i < S::TABLE_WORDS; ++i) tab[i] = table_word<B>(fwd, i);
+    const Table1<B> t1(tab.data());
+    std::vector<uint64_t> image(S::LDS_WORDS + 2 * GUARD, POISON);
     uint64_t* lds = image.data() + GUARD;
-    std::vector<std::array<uint64_t, 32>> v(THREADS);
+    std::vector<std::array<uint64_t, 32>> v(S::THREADS);
     auto intact = [&]() {
         for (int i = 0; i < GUARD; ++i)
-            if (image[i] != POISON || image[GUARD + LDS_WORDS + i] != POISON) return false;
-        for (int t = 0; t < THREADS; ++t)
-            if (lds[T2_OFF + t] != tab[T1_WORDS + t]) return false;
+            if (image[i] != POISON || image[GUARD + S::LDS_WORDS + i] != POISON) return false;
+        for (int t = 0; t < S::T2_WORDS; ++t)
+            if (lds[S::T2_OFF + t] != tab[S::T1_WORDS + t]) return false;
         return true;
     };
-    auto poison = [&]() { std::fill(lds, lds + XBUF_WORDS, POISON); };
+    auto poison = [&]() { std::fill(lds, lds + S::XBUF_WORDS, POISON); };
     for (size_t b = 0; b < blocks; ++b) {
-        for (int t = 0; t < THREADS; ++t) lds[T2_OFF + t] = tab[T1_WORDS + t];
+        for (int t = 0; t < S::T2_WORDS; ++t) lds[S::T2_OFF + t] = tab[S::T1_WORDS + t];
         for (size_t row = b; row < rows; row += blocks) {
-            for (int t = 0; t < THREADS; ++t) {
-                load_row<NZ>(v[t].data(), in, stride, len, row, role(t).m);
+            for (int t = 0; t < S::THREADS; ++t) {
+                load_row<B, NZ>(v[t].data(), in, stride, len, row, role<B>(t).m);
                 gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v[t].data());
             }
             for (int rd = 0; rd < 2; ++rd) {
                 poison();
-                for (int t = 0; t < THREADS; ++t) {
-                    const Role r = role(t);
+                for (int t = 0; t < S::THREADS; ++t) {
+                    const Role r = role<B>(t);
                     const int h = ((t >> 6) & 1) ^ rd;
                     uint64_t tw[8];
-                    load_tw1<0>(tw, t1, h, r.m);
-                    if (h == 0) x1_write<0>(lds, v[t].data(), tw, t1, r.m);
-                    else x1_write<1>(lds, v[t].data(), tw, t1, r.m);
+                    load_tw1<B, 0>(tw, t1, h, r.m);
+                    if (h == 0) x1_write<B, 0>(lds, v[t].data(), tw, t1, r.m);
+                    else x1_write<B, 1>(lds, v[t].data(), tw, t1, r.m);
                 }
-                for (int t = 0; t < THREADS; ++t) {
-                    const Role r = role(t);
-                    if ((((t >> 6) & 1) ^ rd) == 0) x1_read<0>(lds, v[t].data(), r.j1b, r.k3b);
-                    else x1_read<1>(lds, v[t].data(), r.j1b, r.k3b);
+                for (int t = 0; t < S::THREADS; ++t) {
+                    const Role r = role<B>(t);
+                    if ((((t >> 6) & 1) ^ rd) == 0) x1_read<B, 0>(lds, v[t].data(), r.j1b, r.k3b);
+                    else x1_read<B, 1>(lds, v[t].data(), r.j1b, r.k3b);
                 }
             }
-            for (int t = 0; t < THREADS; ++t) gl::dit_pow2<5, gl::E_W32>(v[t].data());
+            for (int t = 0; t < S::THREADS; ++t) gl::dit_pow2<5, gl::E_W32>(v[t].data());
             for (int rd = 0; rd < 2; ++rd) {
                 poison();
-                for (int t = 0; t < THREADS; ++t) {
-                    const Role r = role(t);
-                    if (((t >> 7) ^ rd) == 0) x2_write<0>(lds, v[t].data(), r.j1b, r.k3b);
-                    else x2_write<1>(lds, v[t].data(), r.j1b, r.k3b);
+                for (int t = 0; t < S::THREADS; ++t) {
+                    const Role r = role<B>(t);
+                    if ((((t >> 7) & 1) ^ rd) == 0) x2_write<B, 0>(lds, v[t].data(), r.j1b, r.k3b);
+                    else x2_write<B, 1>(lds, v[t].data(), r.j1b, r.k3b);
                 }
-                for (int t = 0; t < THREADS; ++t) {
-                    const Role r = role(t);
-                    if (((t >> 7) ^ rd) == 0) x2_read<0>(lds, v[t].data(), r.k3c, r.xc);
-                    else x2_read<1>(lds, v[t].data(), r.k3c, r.xc);
+                for (int t = 0; t < S::THREADS; ++t) {
+                    const Role r = role<B>(t);
+                    if ((((t >> 7) & 1) ^ rd) == 0) x2_read<B, 0>(lds, v[t].data(), r.k3c, r.xc);
+                    else x2_read<B, 1>(lds, v[t].data(), r.k3c, r.xc);
                 }
             }
-            for (int t = 0; t < THREADS; ++t) {
-                stage_c(v[t].data());
-                const Role r = role(t);
+            for (int t = 0; t < S::THREADS; ++t) {
+                stage_c<B>(v[t].data());
+                const Role r = role<B>(t);
                 for (int s = 0; s < 32; ++s)
-                    out[row * N + r.k3c + 32 * ((s & 3) + 4 * r.xc) + 1024 * (s >> 2)] = v[t][s];
+                    out[row * S::N + r.k3c + 32 * ((s % S::P) + S::P * r.xc) + 1024 * (s / S::P)] = v[t][s];
             }
             if (!intact()) return -1;
         }
     }
     return 0;
 }
+
+template <int B>
+int rr_dispatch(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t blocks,
+                uint64_t* out) {
+    using S = vmx::rr::Shape<B>;
+    if (len == 0 || len > size_t{S::N} || stride < len) return 1;
+    if (len <= size_t{8} * S::M) return rr_emulate<B, 8>(fwd, in, stride, len, rows, blocks, out);
+    if (len <= size_t{16} * S::M) return rr_emulate<B, 16>(fwd, in, stride, len, rows, blocks, out);
+    return rr_emulate<B, 32>(fwd, in, stride, len, rows, blocks, out);
+}
 }  // namespace
 
-// The kernel's choice of NZ (ntt13r_u64_rows), then the emulation.
+// The kernels' choice of NZ (ntt_rr.hip), then the emulation: n = 2^13 or 2^14.
 extern "C" __attribute__((visibility("default"))) int glc_ntt13r_u64(const uint64_t* fwd, const uint64_t* in,
                                                                      size_t stride, size_t len, size_t rows,
                                                                      size_t blocks, uint64_t* out) {
-    if (len == 0 || len > 8192 || stride < len) return 1;
-    if (len <= 2048) return n13r_emulate<8>(fwd, in, stride, len, rows, blocks, out);
-    if (len <= 4096) return n13r_emulate<16>(fwd, in, stride, len, rows, blocks, out);
-    return n13r_emulate<32>(fwd, in, stride, len, rows, blocks, out);
+    return rr_dispatch<3>(fwd, in, stride, len, rows, blocks, out);
+}
+extern "C" __attribute__((visibility("default"))) int glc_ntt14r_u64(const uint64_t* fwd, const uint64_t* in,
+                                                                     size_t stride, size_t len, size_t rows,
+                                                                     size_t blocks, uint64_t* out) {
+    return rr_dispatch<4>(fwd, in, stride, len, rows, blocks, out);
 }

@@ -36,11 +36,18 @@ int ntt15_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, si
                    TwiddleSet* t);
 int ntt15_msg_rows(Context* c, const int16_t* w, const uint64_t* pads, size_t cols, size_t pad, size_t rows,
                    size_t n, uint64_t* out, TwiddleSet* t);
-// Forward NTT of rows of n = 2^13 canonical u64 in one pass (encode_fast.hip,
-// ntt13r.hpp): row r is in[r * stride .. r * stride + len), zero beyond len
-// (len <= n).  Returns 1 (nothing done) for other sizes, 0 on success, -1 on error.
+// Forward NTT of rows of n = 2^13 (ntt13r) or 2^14 (ntt14r) canonical u64 in
+// one pass (ntt_rr.hip): row r is in[r * stride .. r * stride + len), zero
+// beyond len (len <= n).  Returns 1 (nothing done) for other sizes, 0 on
+// success, -1 on error.
 int ntt13r_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
                     TwiddleSet* t);
+int ntt14r_u64_rows(Context* c, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t n, uint64_t* out,
+                    TwiddleSet* t);
+// The n = 2^13 tables of ntt13r inside the encode's device table (built on
+// first use; null on error), and their builder.
+const uint64_t* enc13_rr_table(Context* c, TwiddleSet* t);
+int build_rr13_table(Context* c, const uint64_t* fwd, uint64_t* tab);
 int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size_t n, uint64_t* out,
                     TwiddleSet* t);
 

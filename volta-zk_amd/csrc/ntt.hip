@@ -166,7 +166,11 @@ int ntt_fp_rows(Context* c, const uint64_t* in, size_t in_stride, size_t msg_len
         const int rc = ntt13r_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
         if (rc <= 0) return rc;
     }
-    // n = 2^15 forward with at most 2^13 nonzero inputs: one pass as well.
+    if (!inverse && n == 16384) {
+        const int rc = ntt14r_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
+        if (rc <= 0) return rc;
+    }
+    // n = 2^15 forward: one pass as well.
     if (!inverse && n == 32768) {
         const int rc = ntt15_u64_rows(c, in, in_stride, msg_len, rows, n, out, t);
         if (rc <= 0) return rc;
