@@ -101,6 +101,29 @@ __host__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
 }
 #endif
 
+// Fold hi 2^64 + lo for hi < 2^32 (hi 2^64 = hi eps): fold128 without the
+// hh 2^96 term, 5 VALU instructions fewer on the device.
+#if defined(__HIP_DEVICE_COMPILE__)
+__device__ __forceinline__ uint64_t fold96(uint64_t lo, uint32_t hi) {
+    uint64_t r, c;
+    asm("v_mad_u64_u32 %0, %1, %2, -1, %3" : "=v"(r), "=s"(c) : "v"(hi), "v"(lo));
+    const uint32_t r0 = static_cast<uint32_t>(r), r1 = static_cast<uint32_t>(r >> 32);
+    uint32_t s0, s1;
+    asm("v_add_co_u32 %0, vcc, -1, %2\n\t"
+        "s_nop 1\n\t"
+        "v_addc_co_u32 %1, vcc, 0, %3, vcc\n\t"
+        "s_or_b64 vcc, vcc, %4\n\t"
+        "v_cndmask_b32 %0, %2, %0, vcc\n\t"
+        "v_cndmask_b32 %1, %3, %1, vcc"
+        : "=&v"(s0), "=&v"(s1)
+        : "v"(r0), "v"(r1), "s"(c)
+        : "vcc", "scc");
+    return (static_cast<uint64_t>(s1) << 32) | s0;
+}
+#else
+__host__ __forceinline__ uint64_t fold96(uint64_t lo, uint32_t hi) { return fold128(lo, hi); }
+#endif
+
 #if defined(__HIP_DEVICE_COMPILE__)
 __device__ __forceinline__ void mul_wide(uint64_t a, uint64_t b, uint64_t& lo, uint64_t& hi) {
     lo = a * b;

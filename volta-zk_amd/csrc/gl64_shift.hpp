@@ -70,7 +70,7 @@ __host__ __device__ __forceinline__ uint64_t shl_mod(uint64_t x) {
     if constexpr (S == 0) {
         return x;
     } else if constexpr (S < 32) {
-        return fold128(x << S, x >> (64 - S));
+        return fold96(x << S, static_cast<uint32_t>(x >> (64 - S)));
     } else if constexpr (S < 64) {
         return shl_mod_hi<S - 32>(x);
     } else {
@@ -146,7 +146,7 @@ __host__ __device__ __forceinline__ uint64_t small_shl_abs(uint32_t ax) {
     if constexpr (S + 16 <= 63) {
         return static_cast<uint64_t>(ax) << S;  // < 2^63 < p
     } else if constexpr (S < 64) {
-        return fold128(static_cast<uint64_t>(ax) << S, static_cast<uint64_t>(ax) >> (64 - S));
+        return fold96(static_cast<uint64_t>(ax) << S, static_cast<uint32_t>(static_cast<uint64_t>(ax) >> (64 - S)));
     } else {
         return shl_mod<S>(static_cast<uint64_t>(ax));
     }
