@@ -17,6 +17,18 @@ namespace gl {
 constexpr uint64_t P = 0xFFFFFFFF00000001ull;
 constexpr uint64_t EPS = 0x00000000FFFFFFFFull;
 
+// A 64-bit value from two 32-bit words, kept as one register pair on the
+// device: written as (hi << 32) | lo, the compiler reads the OR as an add of
+// disjoint halves and splits a later 64-bit add into two adds of zero-extended
+// halves (an extra add and a register copy each time).
+__host__ __device__ __forceinline__ uint64_t pack64(uint32_t lo, uint32_t hi) {
+    uint64_t r = (static_cast<uint64_t>(hi) << 32) | lo;
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("" : "+v"(r));
+#endif
+    return r;
+}
+
 // ---- host/device scalar ops (canonical in, canonical out) ---------------
 
 __host__ __device__ __forceinline__ uint64_t canon(uint64_t x) { return x >= P ? x - P : x; }
@@ -39,7 +51,7 @@ __host__ __device__ __forceinline__ uint64_t sub(uint64_t a, uint64_t b) {
     const uint32_t e = b1 ? 0xFFFFFFFFu : 0u;
     const uint32_t r0 = __builtin_subc(d0, e, 0u, &e0);
     const uint32_t r1 = d1 - e0;
-    return (static_cast<uint64_t>(r1) << 32) | r0;
+    return pack64(r0, r1);
 }
 
 __host__ __device__ __forceinline__ uint64_t neg(uint64_t a) { return a ? P - a : 0; }
@@ -86,7 +98,7 @@ __device__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
         : "=&v"(s0), "=&v"(s1)
         : "v"(r0), "v"(r1), "s"(c)
         : "vcc", "scc");
-    return (static_cast<uint64_t>(s1) << 32) | s0;
+    return pack64(s0, s1);
 }
 #else
 __host__ __forceinline__ uint64_t fold128(uint64_t lo, uint64_t hi) {
@@ -118,7 +130,7 @@ __device__ __forceinline__ uint64_t fold96(uint64_t lo, uint32_t hi) {
         : "=&v"(s0), "=&v"(s1)
         : "v"(r0), "v"(r1), "s"(c)
         : "vcc", "scc");
-    return (static_cast<uint64_t>(s1) << 32) | s0;
+    return pack64(s0, s1);
 }
 #else
 __host__ __forceinline__ uint64_t fold96(uint64_t lo, uint32_t hi) { return fold128(lo, hi); }

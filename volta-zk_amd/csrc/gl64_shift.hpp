@@ -59,7 +59,7 @@ __host__ __device__ __forceinline__ uint64_t shl_mod_hi(uint64_t x) {
     const uint32_t chi = cb | c2;
     const uint32_t r0 = __builtin_subc(0u, clo, 0u, &b0);  // r = h 2^32 - C
     const uint32_t r1 = __builtin_subc(h, chi, b0, &b1);
-    const uint64_t r = (static_cast<uint64_t>(r1) << 32) | r0;
+    const uint64_t r = pack64(r0, r1);
     return b1 ? r - EPS : r;  // negative: + p = - eps mod 2^64
 }
 
