@@ -634,3 +634,51 @@ def test_ntt14_one_pass_device_rows(backend, oracle, rows):
     want = oracle.ntt_encode_batch(host, n)
     bad = np.nonzero((got != want).any(axis=1))[0]
     assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
+
+
+@pytest.mark.parametrize("bits", [19, 20])
+def test_batched_last_pass_reads_the_n_word_table(oracle, bits):
+    """A batch of at least 16 transforms of 2^19 .. 2^24 points runs its last
+    column pass from an n-word pre-twiddle table (times n^-1 for the inverse),
+    with every row's copy of a tile dispatched back to back.  Forward and
+    inverse against the oracle, the same rows as a 15-row batch (the two-level
+    table path), an Fp2 batch of 16 rows, and a second call that allocates
+    nothing."""
+    from volta_mi355x import FP2, Backend
+    n = 1 << bits
+    host = rand_fp(1900 + bits, (16, n))
+    want = oracle.ntt_forward_batch(host)
+    want_inv = oracle.ntt_inverse_batch(host)
+    with Backend() as b:
+        inp = b.upload_device(host.reshape(-1))
+        out = b.ntt_fp_batch_device(inp, 16, n)
+        assert (b.download_device(out).reshape(16, n) == want).all()
+        inv = b.ntt_fp_inverse_batch_device(inp, 16, n)
+        assert (b.download_device(inv).reshape(16, n) == want_inv).all()
+        # the same transforms again: the tables are cached
+        before = b.get_stats()
+        for x in (out, inv):
+            b.free_device(x)
+        out = b.ntt_fp_batch_device(inp, 16, n)
+        inv = b.ntt_fp_inverse_batch_device(inp, 16, n)
+        after = b.get_stats()
+        assert after["allocation_calls"] == before["allocation_calls"]
+        assert (b.download_device(out).reshape(16, n) == want).all()
+        assert (b.download_device(inv).reshape(16, n) == want_inv).all()
+        # fifteen rows take the two-level table
+        part = b.ntt_fp_batch_device(inp, 15, n)
+        assert (b.download_device(part).reshape(15, n) == want[:15]).all()
+        part_inv = b.ntt_fp_inverse_batch_device(inp, 15, n)
+        assert (b.download_device(part_inv).reshape(15, n) == want_inv[:15]).all()
+        # Fp2 rows: both coordinates through the base-field table
+        h2 = rand_fp(2900 + bits, (16, n, 2))
+        d2 = b.alloc_device(16 * n, FP2)
+        b.upload_into(d2, 0, h2.reshape(-1))
+        o2 = b.ntt_fp2_batch_device(d2, 16, n)
+        got2 = b.download_device(o2).view(np.uint64).reshape(16, n, 2)
+        for comp in (0, 1):
+            assert (got2[:, :, comp] == oracle.ntt_forward_batch(h2[:, :, comp].copy())).all()
+        ws, res, cached = b.memory_breakdown()
+        assert ws + res + cached == b.get_stats()["live_device_bytes"]
+        for x in (inp, out, inv, part, part_inv, d2, o2):
+            b.free_device(x)

@@ -816,6 +816,8 @@ VMX_API void volta_cuda_destroy(void* raw) {
             if (kv.second.reg) (void)hipFree(kv.second.reg);
             for (uint64_t* t : kv.second.col)
                 if (t) (void)hipFree(t);
+            for (uint64_t* t : kv.second.col_scaled)
+                if (t) (void)hipFree(t);
         }
         for (auto& p : c->pinned) {
             if (p.ready) (void)hipEventDestroy(p.ready);

@@ -212,6 +212,9 @@ struct TwiddleSet {
     // points (derived on the device): col[rb][i 2^(log2 n - rb) + l] = w^(i l),
     // i < 2^rb.  col_bytes sums them.
     uint64_t* col[16] = {};
+    // The same tables times n^-1 (n = their span), for the last pass of a
+    // batched inverse transform; col_bytes counts them too.
+    uint64_t* col_scaled[16] = {};
     size_t col_bytes = 0;
     size_t n = 0;
 };
