@@ -51,16 +51,18 @@ constexpr size_t TABLE_BYTES = R13_OFF + size_t{rr::Shape<3>::TABLE_WORDS} * siz
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Phase B's LDS half for row j1 and output parity H: reads Y's row and applies
-// the first radix-2 stage; the 32-point DFT over v then gives X[2k + H] in v[k].
+// Phase B's LDS half for row j1 and output parity H.  Phase A stored the first
+// radix-2 stage's sums and differences, S[q] = Y[q] + Y[q + 32] in columns
+// 0..31 of the row and D[q] = Y[q] - Y[q + 32] in columns 32..63; parity 0
+// takes S, parity 1 takes D times w64^q, and the 32-point DFT over v then
+// gives X[2k + H] in v[k].
 template <int H>
 __host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1, uint64_t* v) {
-    const uint64_t* y = Y + j1 * PITCH;
+    const uint64_t* y = Y + j1 * PITCH + 32 * H;
     gl::static_for<0, 32>([&](auto qq) {
         constexpr int q = decltype(qq)::value;
-        const uint64_t a = y[q], b = y[q + 32];
-        if constexpr (H == 0) v[gl::bitrev_c(q, 5)] = gl::add(a, b);
-        else v[gl::bitrev_c(q, 5)] = gl::mul_pow2<gl::E_W64 * q>(gl::sub(a, b));
+        if constexpr (H == 0) v[gl::bitrev_c(q, 5)] = y[q];
+        else v[gl::bitrev_c(q, 5)] = gl::mul_pow2<gl::E_W64 * q>(y[q]);
     });
 }
 
@@ -193,11 +195,19 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
                         d[P + 1][t][h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[P + 1][h], xf[t], c[P + 1][h], 0, 0, 0);
             }
             const int j1 = 4 * (q0 + P) + grp;
+            uint64_t y[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int a[4] = {d[P][t][0][0], d[P][t][0][1], d[P][t][0][2], d[P][t][0][3]};
                 const int b[4] = {d[P][t][1][0], d[P][t][1][1], d[P][t][1][2], d[P][t][1][3]};
-                Y[j1 * PITCH + 16 * t + m] = gl::mul32x4(enc13m::recombine(a, b, k16, keps), g[P][t]);
+                y[t] = gl::mul32x4(enc13m::recombine(a, b, k16, keps), g[P][t]);
+            }
+            // columns i2 = 16 t + m and i2 + 32 (t + 2) of row j1 are both in
+            // this lane: store phase B's first-stage sums and differences
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                Y[j1 * PITCH + 16 * t + m] = gl::add(y[t], y[t + 2]);
+                Y[j1 * PITCH + 32 + 16 * t + m] = gl::sub(y[t], y[t + 2]);
             }
             __builtin_amdgcn_sched_barrier(0);  // at most two pairs' products in registers
         }
