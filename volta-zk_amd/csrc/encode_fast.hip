@@ -24,6 +24,7 @@
 
 #include "context.hpp"
 #include "enc13_mfma.hpp"
+#include "enc13_phase_b.hpp"
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
 #include "kernels.hpp"
@@ -51,33 +52,19 @@ constexpr size_t TABLE_BYTES = R13_OFF + size_t{rr::Shape<3>::TABLE_WORDS} * siz
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Phase B's LDS half for row j1 and output parity H.  Phase A stored the first
-// radix-2 stage's sums and differences, S[q] = Y[q] + Y[q + 32] in columns
-// 0..31 of the row and D[q] = Y[q] - Y[q + 32] in columns 32..63; parity 0
-// takes S, parity 1 takes D times w64^q, and the 32-point DFT over v then
-// gives X[2k + H] in v[k].
-template <int H>
-__host__ __device__ __forceinline__ void phase_b_first(const uint64_t* Y, int j1, uint64_t* v) {
-    const uint64_t* y = Y + j1 * PITCH + 32 * H;
-    gl::static_for<0, 32>([&](auto qq) {
-        constexpr int q = decltype(qq)::value;
-        if constexpr (H == 0) v[gl::bitrev_c(q, 5)] = y[q];
-        else v[gl::bitrev_c(q, 5)] = gl::mul_pow2<gl::E_W64 * q>(y[q]);
-    });
-}
-
 // Phase B of one row: the 64-point DFT over i2 of Y's row j1 at output parity
-// H, X[2k + H] stored to o[j1 + N1 (2k + H)].  The workgroup's second barrier
-// sits between the LDS reads and the DFT: Y is rewritten by the next row's
-// phase A, and once every wave holds its rows' first stage in registers the
-// workgroup may move on, so the DFTs and stores overlap the next phase A of
-// faster waves.
+// H, X[2k + H] stored to o[j1 + N1 (2k + H)].  Phase A stored the first
+// radix-2 stage's sums S in columns 0..31 of the row and its differences D in
+// columns 32..63.  The workgroup's second barrier sits between the LDS reads
+// and the DFT: Y is rewritten by the next row's phase A, and once every wave
+// holds its row's inputs in registers the workgroup may move on, so the DFTs
+// and stores overlap the next phase A of faster waves.
 __device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, int H, uint64_t* o) {
     uint64_t v[K];
-    if (H == 0) phase_b_first<0>(Y, j1, v);
-    else phase_b_first<1>(Y, j1, v);
+    if (H == 0) enc13m::phase_b_load<0>(Y + j1 * PITCH, v);
+    else enc13m::phase_b_load<1>(Y + j1 * PITCH + 32, v);
     __syncthreads();
-    gl::dit_pow2<5, gl::E_W32>(v);
+    enc13m::phase_b_dft(v);
     o += j1 + N1 * H;
 #pragma unroll
     for (int k = 0; k < 32; ++k) __builtin_nontemporal_store(v[k], o + N1 * 2 * k);

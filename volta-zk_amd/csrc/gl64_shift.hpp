@@ -86,12 +86,27 @@ __host__ __device__ __forceinline__ uint64_t shl_mod_neg(uint64_t x) {
     return shr_mod<96 - S>(x);
 }
 
-// x * 2^E mod p for any E >= 0 (reduced mod 192; E mod 192 >= 96 negates).
+// x * 2^E up to sign, in its cheapest form: with S = (E mod 192) mod 96,
+// 2^E = +-2^S, and for S >= 64 the division form yields -(x 2^S) directly.
+// pow2_neg(E) tells whether the result holds -(x 2^E) rather than x 2^E.
+constexpr bool pow2_neg(int E) {
+    const int e = E % 192;
+    return (e >= 96) != (e % 96 >= 64);
+}
+
+template <int E>
+__host__ __device__ __forceinline__ uint64_t mul_pow2_signed(uint64_t x) {
+    constexpr int S = (E % 192) % 96;
+    if constexpr (S >= 64) return shr_mod<96 - S>(x);
+    else return shl_mod<S>(x);
+}
+
+// x * 2^E mod p for any E >= 0.
 template <int E>
 __host__ __device__ __forceinline__ uint64_t mul_pow2(uint64_t x) {
-    constexpr int e = E % 192;
-    if constexpr (e >= 96) return neg(shl_mod<e - 96>(x));
-    else return shl_mod<e>(x);
+    const uint64_t t = mul_pow2_signed<E>(x);
+    if constexpr (pow2_neg(E)) return neg(t);
+    else return t;
 }
 
 // DIT butterfly (u, v) <- (u + w v, u - w v) with w = 2^E.

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "enc13_mfma.hpp"
+#include "enc13_phase_b.hpp"
 #include "gl64.hpp"
 #include "gl64_shift.hpp"
 #include "ntt_rr.hpp"
@@ -102,6 +103,18 @@ extern "C" __attribute__((visibility("default"))) void glc_enc13_phase_a(const u
                 const uint64_t g = e < 4096 ? tw_half[e] : gl::neg(tw_half[e - 4096]);
                 Y[j1 * 64 + i2] = gl::mul32x4(enc13m::recombine(acc, acc + 4), g);
             }
+}
+
+// Phase B of one row as the encode kernel runs it: y holds the row's 64 values
+// Y[i2] (canonical), out receives X[2k + H] for k < 32.  The sums and
+// differences are phase A's stores.
+extern "C" __attribute__((visibility("default"))) void glc_enc13_phase_b(const uint64_t* y, int H, uint64_t* out) {
+    uint64_t sd[32], v[32];
+    for (int q = 0; q < 32; ++q) sd[q] = H == 0 ? gl::add(y[q], y[q + 32]) : gl::sub(y[q], y[q + 32]);
+    if (H == 0) enc13m::phase_b_load<0>(sd, v);
+    else enc13m::phase_b_load<1>(sd, v);
+    enc13m::phase_b_dft(v);
+    for (int k = 0; k < 32; ++k) out[k] = v[k];
 }
 
 // ---- the one-pass 2^15 transform (ntt15.hip), emulated on the host ----------
