@@ -527,6 +527,36 @@ def test_ntt13_one_pass_device_rows(backend, oracle, rows):
     assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
 
 
+@pytest.mark.parametrize("bits", [13, 14])
+def test_one_pass_device_rows_with_zero_tails(backend, oracle, bits):
+    """Rows passed at full length (read whole: the caller may have written
+    them) that are zero from 8 M on (M = n / 32), as message rows are: each
+    wave of the one-pass kernel checks its inputs there and runs stage A's
+    first two stages as copies when they are all zero.  Most rows have that
+    tail, some carry one nonzero value at a position that falls to a different
+    wave each time, a few are dense."""
+    n = 1 << bits
+    m8 = 8 * (n // 32)
+    rows = 300
+    host = rand_fp(4400 + bits, (rows, n))
+    host[:, m8:] = 0
+    host[0, :4] = [0, 1, P - 1, P - 2]
+    for r in range(1, 40):
+        host[r, m8 + (r * 97) % (n - m8)] = P - 1 - r
+    host[40:44] = rand_fp(4500 + bits, (4, n))
+    host[44, n - 1] = 1
+    d = backend.upload_device(host.reshape(-1))
+    dout = backend.alloc_device(rows * n, np.uint64)
+    assert backend.lib.volta_cuda_ntt_fp_batch_device(backend.raw, d.id, 0, rows, n, dout.id, 0) == 0, \
+        backend.last_error()
+    got = backend.download_device(dout).reshape(rows, n)
+    for b in (d, dout):
+        backend.free_device(b)
+    want = oracle.ntt_forward_batch(host)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
+
+
 @pytest.mark.parametrize("msg_len", [1, 5, 2047, 2048, 2049, 4096, 8191, 8192])
 def test_ntt13_one_pass_host_batch_lengths(backend, oracle, msg_len):
     """The host batch (volta_cuda_ntt_fp_batch, compact rows of msg_len, the

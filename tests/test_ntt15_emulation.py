@@ -144,3 +144,36 @@ def test_ntt14_rows_match_the_oracle(glc, fwd14, length, stride):
     got = np.zeros((rows, N14), dtype=np.uint64)
     assert glc.glc_ntt14r_u64(_p(fwd14), _p(src), stride, length, rows, blocks, _p(got)) == 0
     assert (got == want).all()
+
+
+@pytest.mark.parametrize("log_n", [13, 14])
+def test_rows_read_in_full_with_zero_tails(glc, fwd13, fwd14, log_n):
+    """Rows passed at full length (the kernels read them whole) whose values
+    are zero from 8 M on (M = n / 32: 2048 at 2^13, 4096 at 2^14), as message
+    rows are: a wave whose inputs are all zero there runs stage A's first two
+    stages as copies.  Row 0 has that tail zero (every wave copies), row 1 one
+    nonzero value at 8 M + 5 (only the wave holding it runs them in full), row 2
+    is dense, row 3 nonzero only at n - 1; every row against the oracle, and
+    the waves of each kind counted."""
+    n = 1 << log_n
+    fn = glc.glc_ntt13r_u64 if log_n == 13 else glc.glc_ntt14r_u64
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_size_t] * 4 + [ctypes.c_void_p]
+    glc.glc_rr_wave_counts.restype = None
+    glc.glc_rr_wave_counts.argtypes = [ctypes.POINTER(ctypes.c_long), ctypes.POINTER(ctypes.c_long), ctypes.c_int]
+    m8 = 8 * (n // 32)
+    rng = np.random.default_rng(log_n + 100)
+    src = np.zeros((4, n), dtype=np.uint64)
+    src[:, :m8] = _field(rng, (4, m8))
+    src[0, :4] = np.array([0, 1, P - 1, P - 2], dtype=np.uint64)
+    src[1, m8 + 5] = P - 1
+    src[2] = _field(rng, (1, n))[0]
+    src[3, n - 1] = 12345
+    full, copy = ctypes.c_long(), ctypes.c_long()
+    glc.glc_rr_wave_counts(ctypes.byref(full), ctypes.byref(copy), 1)
+    got = np.zeros((4, n), dtype=np.uint64)
+    assert fn(_p(fwd13 if log_n == 13 else fwd14), _p(src), n, n, 4, 2, _p(got)) == 0
+    assert (got == oracle.ntt_forward_batch(src)).all()
+    glc.glc_rr_wave_counts(ctypes.byref(full), ctypes.byref(copy), 1)
+    waves = (n // 32) // 64
+    assert (full.value, copy.value) == (1 + waves + 1, waves + 2 * (waves - 1))

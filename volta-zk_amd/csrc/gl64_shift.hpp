@@ -249,10 +249,11 @@ constexpr uint64_t dit_mask_next(uint64_t m, int len, int n) {
 // MASK (bit i: v[i] may be nonzero; the other positions must hold 0).  A
 // butterfly whose second input is known zero is the copy (u, u), one whose
 // inputs are both known zero is skipped, so a zero tail of the input costs no
-// arithmetic in the stages it reaches.
-template <int LOG, int EW, uint64_t MASK, int LEN = 2>
+// arithmetic in the stages it reaches.  Runs the stages of spans LEN, 2 LEN,
+// ... below STOP (all of them by default).
+template <int LOG, int EW, uint64_t MASK, int LEN = 2, int STOP = (2 << LOG)>
 __host__ __device__ __forceinline__ void dit_pow2_sparse(uint64_t* v) {
-    if constexpr (LEN <= (1 << LOG)) {
+    if constexpr (LEN <= (1 << LOG) && LEN < STOP) {
         constexpr int N = 1 << LOG;
         constexpr int HALF = LEN / 2;
         static_for<0, N / LEN>([&](auto g) {
@@ -267,7 +268,7 @@ __host__ __device__ __forceinline__ void dit_pow2_sparse(uint64_t* v) {
                 }
             });
         });
-        dit_pow2_sparse<LOG, EW, dit_mask_next(MASK, LEN, N), LEN * 2>(v);
+        dit_pow2_sparse<LOG, EW, dit_mask_next(MASK, LEN, N), LEN * 2, STOP>(v);
     }
 }
 

@@ -228,8 +228,11 @@ extern "C" __attribute__((visibility("default"))) int glc_ntt15_msg(const uint64
 // ---- the one-pass 2^13 / 2^14 transforms (ntt_rr.hip), emulated ---------------------
 // As for the 2^15 transform: the workgroup's threads run the phases one after
 // the other between the kernel's barriers, on a poisoned exchange buffer with
-// guard words.
+// guard words.  Rows read in full (NZ = 32) take stage A's first two stages
+// per wave of 64 threads as the kernel does: copies when the wave's inputs are
+// all zero from 8 M on, in full otherwise; the waves of each kind are counted.
 namespace {
+long g_rr_waves_full = 0, g_rr_waves_copy = 0;
 template <int B, int NZ>
 int rr_emulate(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t len, size_t rows, size_t blocks,
                uint64_t* out) {
@@ -254,9 +257,21 @@ int rr_emulate(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t le
     for (size_t b = 0; b < blocks; ++b) {
         for (int t = 0; t < S::T2_WORDS; ++t) lds[S::T2_OFF + t] = tab[S::T1_WORDS + t];
         for (size_t row = b; row < rows; row += blocks) {
-            for (int t = 0; t < S::THREADS; ++t) {
-                load_row<B, NZ>(v[t].data(), in, stride, len, row, role<B>(t).m);
-                gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v[t].data());
+            for (int t = 0; t < S::THREADS; ++t) load_row<B, NZ>(v[t].data(), in, stride, len, row, role<B>(t).m);
+            if constexpr (NZ == 32) {
+                for (int w0 = 0; w0 < S::THREADS; w0 += 64) {
+                    bool tail = false;
+                    for (int t = w0; t < w0 + 64; ++t)
+                        for (int j3 = 8; j3 < 32; ++j3) tail = tail || v[t][gl::bitrev_c(j3, 5)] != 0;
+                    ++(tail ? g_rr_waves_full : g_rr_waves_copy);
+                    for (int t = w0; t < w0 + 64; ++t) {
+                        if (tail) gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(32), 2, 8>(v[t].data());
+                        else gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(8), 2, 8>(v[t].data());
+                        gl::dit_pow2<5, gl::E_W32, 8>(v[t].data());
+                    }
+                }
+            } else {
+                for (int t = 0; t < S::THREADS; ++t) gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v[t].data());
             }
             for (int rd = 0; rd < 2; ++rd) {
                 poison();
@@ -310,6 +325,14 @@ int rr_dispatch(const uint64_t* fwd, const uint64_t* in, size_t stride, size_t l
     return rr_emulate<B, 32>(fwd, in, stride, len, rows, blocks, out);
 }
 }  // namespace
+
+// Waves of rows read in full that ran stage A's first two stages in full /
+// as copies, since the last reset.
+extern "C" __attribute__((visibility("default"))) void glc_rr_wave_counts(long* full, long* copy, int reset) {
+    *full = g_rr_waves_full;
+    *copy = g_rr_waves_copy;
+    if (reset) g_rr_waves_full = g_rr_waves_copy = 0;
+}
 
 // The kernels' choice of NZ (ntt_rr.hip), then the emulation: n = 2^13 or 2^14.
 extern "C" __attribute__((visibility("default"))) int glc_ntt13r_u64(const uint64_t* fwd, const uint64_t* in,

@@ -41,7 +41,23 @@ __global__ __launch_bounds__(Shape<B>::THREADS, Shape<B>::WAVES_PER_SIMD) void r
     for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
         uint64_t v[32], tw[8];
         load_row<B, NZ>(v, in, stride, len, row, here().m);
-        gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v);
+        if constexpr (NZ == 32) {
+            // Rows the length does not bound (a buffer the caller may have
+            // written through a device pointer) are often still zero from
+            // 8 M on (message rows).  A wave whose inputs are all zero there
+            // takes the first two stages as the copies dit_pow2_sparse makes
+            // for NZ = 8; any nonzero value in the wave runs them in full.
+            // Both give the same values on such rows.
+            uint64_t tail = 0;
+            gl::static_for<8, 32>([&](auto j_) { tail |= v[gl::bitrev_c(decltype(j_)::value, 5)]; });
+            if (__builtin_amdgcn_ballot_w64(tail != 0) != 0)
+                gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(32), 2, 8>(v);
+            else
+                gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(8), 2, 8>(v);
+            gl::dit_pow2<5, gl::E_W32, 8>(v);
+        } else {
+            gl::dit_pow2_sparse<5, gl::E_W32, prefix_mask(NZ)>(v);
+        }
         __builtin_amdgcn_sched_barrier(0);
         {
             const Role q = here();
