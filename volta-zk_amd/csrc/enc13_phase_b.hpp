@@ -27,6 +27,15 @@ __host__ __device__ __forceinline__ void phase_b_load(const uint64_t* sd, uint64
     });
 }
 
+// Parity 1's pre-twiddle applied in place, to S-or-D words loaded as for
+// parity 0: v[bitrev q] = D[q] -> D[q] w64^q.
+__host__ __device__ __forceinline__ void phase_b_twiddle(uint64_t* v) {
+    gl::static_for<1, 32>([&](auto qq) {
+        constexpr int q = decltype(qq)::value;
+        v[gl::bitrev_c(q, 5)] = gl::mul_pow2<gl::E_W64 * q>(v[gl::bitrev_c(q, 5)]);
+    });
+}
+
 // The 32-point DFT: v[k] = X[2k + H].
 __host__ __device__ __forceinline__ void phase_b_dft(uint64_t* v) { gl::dit_pow2<5, gl::E_W32>(v); }
 

@@ -41,6 +41,7 @@ constexpr int N2 = 64;     // i2 range
 constexpr int K = 32;      // non-zero i1 range (cols <= K * N2 = 2048)
 constexpr int PITCH = 65;  // u64 per LDS row of Y
 constexpr int THREADS = 256;
+constexpr size_t LATE_ROWS = 8;  // rows per workgroup up to which phase B takes the late shifts
 constexpr size_t LDS_BYTES = size_t{N1} * PITCH * sizeof(uint64_t);
 constexpr size_t GRID_BYTES = size_t{N1} * N2 * sizeof(uint64_t);
 // The twiddle grid, then phase A's A fragments, then its accumulator init
@@ -58,12 +59,23 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // columns 32..63.  The workgroup's second barrier sits between the LDS reads
 // and the DFT: Y is rewritten by the next row's phase A, and once every wave
 // holds its row's inputs in registers the workgroup may move on, so the DFTs
-// and stores overlap the next phase A of faster waves.
+// and stores overlap the next phase A of faster waves.  Parity 1's 31 shifts
+// (D[q] w64^q) come before the barrier (LATE = false), where the parity-0
+// wave's wait is filled by the other workgroup's wave on its SIMD when
+// workgroups walk many rows, or after it (LATE = true), so both parities reach
+// the barrier together, which pays when each workgroup has only a few rows.
+template <bool LATE>
 __device__ __forceinline__ void phase_b(const uint64_t* Y, int j1, int H, uint64_t* o) {
     uint64_t v[K];
-    if (H == 0) enc13m::phase_b_load<0>(Y + j1 * PITCH, v);
-    else enc13m::phase_b_load<1>(Y + j1 * PITCH + 32, v);
-    __syncthreads();
+    if constexpr (LATE) {
+        enc13m::phase_b_load<0>(Y + j1 * PITCH + 32 * H, v);
+        __syncthreads();
+        if (H != 0) enc13m::phase_b_twiddle(v);
+    } else {
+        if (H == 0) enc13m::phase_b_load<0>(Y + j1 * PITCH, v);
+        else enc13m::phase_b_load<1>(Y + j1 * PITCH + 32, v);
+        __syncthreads();
+    }
     enc13m::phase_b_dft(v);
     o += j1 + N1 * H;
 #pragma unroll
@@ -102,6 +114,7 @@ __device__ __forceinline__ void load_frags(const int16_t* wr, size_t cols, int l
 // no lane diverges.  The workgroup walks rows blockIdx.x,
 // blockIdx.x + gridDim.x, ..., loading the next row's inputs before phase B of
 // the current row.
+template <bool LATE>
 __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w, size_t cols, size_t rows,
                                             const uint64_t* __restrict__ grid, const v4i* __restrict__ frags,
                                             const v4i* __restrict__ init, uint64_t* __restrict__ out, uint64_t* Y,
@@ -202,11 +215,12 @@ __device__ __forceinline__ void encode_rows(int S, const int16_t* __restrict__ w
         if (next < rows) load_frags(w + next * cols, cols, lane, xf);
         __syncthreads();
         __builtin_amdgcn_s_setprio(0);
-        phase_b(Y, j1b, H, out + row * N);
+        phase_b<LATE>(Y, j1b, H, out + row * N);
         H ^= 1;
     }
 }
 
+template <bool LATE>
 __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __restrict__ w, size_t cols, size_t rows,
                                                           const uint64_t* __restrict__ tables,
                                                           uint64_t* __restrict__ out, uint32_t k16, uint32_t keps) {
@@ -214,7 +228,7 @@ __global__ __launch_bounds__(THREADS, 2) void encode13_i16(const int16_t* __rest
     const int lane = threadIdx.x & 63;
     const v4i* frags = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(tables) + GRID_BYTES);
     const v4i* init = reinterpret_cast<const v4i*>(reinterpret_cast<const unsigned char*>(frags) + enc13m::FRAG_BYTES);
-    encode_rows(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane, k16,
+    encode_rows<LATE>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6), w, cols, rows, tables, frags, init, out, Y, lane, k16,
                 keps);
 }
 
@@ -261,18 +275,27 @@ int encode_i16_fast(Context* c, const int16_t* w, size_t rows, size_t cols, size
         return 1;
     if (rows == 0) return 0;
     if (ensure_grid_twiddles(c, t, enc13::TABLE_BYTES, enc13::build_grid)) return -1;
-    // The LDS limit is an attribute of the kernel on the current device: set
-    // it on every call (a host-side call of about a microsecond), so no flag
-    // shared between contexts, threads or devices is needed.
-    VMX_HIP(c, hipFuncSetAttribute(reinterpret_cast<const void*>(enc13::encode13_i16),
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(enc13::LDS_BYTES)));
     // Two workgroups fit a CU (LDS); a persistent grid of that many overlaps
     // each row's input loads with the previous row's phase B.
     const size_t per_cu = 2;
     const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
     const unsigned blocks = static_cast<unsigned>(std::min(rows, per_cu * cus));
-    hipLaunchKernelGGL(enc13::encode13_i16, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream, w, cols,
-                       rows, static_cast<const uint64_t*>(t->grid), out, 65536u, 0xFFFFFFFFu);
+    // Where parity 1's shifts go (phase_b): after the barrier when each
+    // workgroup walks at most LATE_ROWS rows.
+    const bool late = rows <= enc13::LATE_ROWS * blocks;
+    const void* k = late ? reinterpret_cast<const void*>(enc13::encode13_i16<true>)
+                         : reinterpret_cast<const void*>(enc13::encode13_i16<false>);
+    // The LDS limit is an attribute of the kernel on the current device: set
+    // it on every call (a host-side call of about a microsecond), so no flag
+    // shared between contexts, threads or devices is needed.
+    VMX_HIP(c, hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(enc13::LDS_BYTES)));
+    const uint64_t* grid = t->grid;
+    if (late)
+        hipLaunchKernelGGL(enc13::encode13_i16<true>, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream,
+                           w, cols, rows, grid, out, 65536u, 0xFFFFFFFFu);
+    else
+        hipLaunchKernelGGL(enc13::encode13_i16<false>, dim3(blocks), dim3(enc13::THREADS), enc13::LDS_BYTES, c->stream,
+                           w, cols, rows, grid, out, 65536u, 0xFFFFFFFFu);
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
