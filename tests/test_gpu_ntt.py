@@ -402,6 +402,25 @@ def test_fast_encode_byte_split_edges(backend, oracle, cols, kind):
     assert (got == oracle.pcs_encode_i16(w, None, rows, cols, 0, n)).all()
 
 
+@pytest.mark.parametrize("rows", [4096, 4097, 8200])
+def test_fast_encode_both_phase_b_orders(backend, oracle, rows):
+    """The n = 2^13 fast path puts parity 1's shifts after phase B's barrier
+    when each workgroup walks at most 8 rows (4,096 rows on 256 CUs) and
+    before it otherwise: rows on both sides of that bound, every element
+    against the oracle, through the reference's two calls."""
+    cols, n = 2048, 8192
+    w = np.random.Generator(np.random.PCG64(rows)).integers(-32768, 32768, size=rows * cols, dtype=np.int16)
+    dw, dp = backend.upload_device(w), backend.alloc_device(1, np.uint64)
+    msgs = backend.pcs_messages_device(dw, 0, dp, 0, rows, cols, 0, n)
+    enc = backend.ntt_fp_batch_device(msgs, rows, n)
+    got = backend.download_device(enc).reshape(rows, n)
+    for b in (dw, dp, msgs, enc):
+        backend.free_device(b)
+    want = oracle.pcs_encode_i16(w, None, rows, cols, 0, n)
+    bad = np.nonzero((got != want).any(axis=1))[0]
+    assert bad.size == 0, f"rows {bad[:8].tolist()} differ"
+
+
 # ---- benchmark configurations ---------------------------------------------------------
 
 def test_c1_full_config(backend, oracle):
