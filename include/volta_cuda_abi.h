@@ -364,9 +364,11 @@ int volta_mi355x_pcs_encode_device(void* ctx, uint64_t w_id, size_t w_off, uint6
 /* volta_cuda_pcs_combine_rows_device without any allocation.  No counterpart
  * in the reference: it is for callers that cannot allocate (tight serving
  * loops, harnesses that forbid hipMalloc).  Its partial sums live in a fixed
- * 16 MiB device array per GPU (held until the process ends); a combination
- * whose partials need more is refused with an error (C3's two combinations
- * need 8 MiB).  All contexts on one GPU share the array; the library orders
+ * 16 MiB device array per GPU (held until the process ends).  A combination
+ * whose partials need more at the usual row chunks (C3's two combinations
+ * need 8 MiB) runs with larger chunks, up to 2^16 rows each, and is refused
+ * with an error only when even those need more (2^17 rows of 2048 columns:
+ * above 256 combinations).  All contexts on one GPU share the array; the library orders
  * their uses on the device with a per-device event, so back-to-back calls
  * from different contexts do not race, and each call rewrites every scratch
  * word it reads.  Refused while the context stream is being captured into a

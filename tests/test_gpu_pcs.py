@@ -80,16 +80,15 @@ def test_combine_rows_with_zero_coefficient_chunks(backend, oracle, rows, cols, 
     got = backend.download_device(out).view(np.uint64).reshape(comb, cols + pad, 2)
     assert (got == want).all()
     # the allocation-free entry, twice: its scratch holds the previous call's
-    # partials (the two 4096-row shapes need more partials than it holds)
+    # partials (the two 4096-row shapes need more partials than it holds at
+    # the default row chunks, so they run with larger ones, zero chunks still
+    # skipped)
     out2 = backend.alloc_device(comb * (cols + pad), FP2)
     for _ in range(2):
         rc = backend.lib.volta_mi355x_pcs_combine_rows_device_noalloc(
             backend.raw, dw.id, 0, dp.id, 0, dc.id, 0, rows, cols, pad, comb, out2.id, 0)
-        if rows == 4096:
-            assert rc != 0 and "scratch" in backend.last_error()
-        else:
-            assert rc == 0, backend.last_error()
-            assert (backend.download_device(out2).view(np.uint64).reshape(comb, cols + pad, 2) == want).all()
+        assert rc == 0, backend.last_error()
+        assert (backend.download_device(out2).view(np.uint64).reshape(comb, cols + pad, 2) == want).all()
     for b in (dw, dp, dc, out, out2):
         backend.free_device(b)
 

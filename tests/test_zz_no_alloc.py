@@ -4,7 +4,9 @@
 
 Two calls in a row, the second smaller, so the second runs over scratch the
 first left behind; neither call may allocate (RawStats allocation_calls and
-live_device_bytes unchanged); a plan beyond the fixed scratch is refused."""
+live_device_bytes unchanged); a plan whose partials outgrow the fixed scratch
+at the default row chunks runs with larger ones; a plan beyond it even at the
+largest chunks is refused."""
 import numpy as np
 import pytest
 
@@ -27,7 +29,8 @@ def call(b, name, w, dp, dc, rows, cols, pad, comb, out):
 
 
 @pytest.mark.parametrize("shapes", [[(4096, 2048, 512, 2), (300, 100, 7, 3)],
-                                    [(1 << 16, 2048, 0, 2), (5, 3, 1, 1)]])
+                                    [(1 << 16, 2048, 0, 2), (5, 3, 1, 1)],
+                                    [(1 << 17, 2048, 0, 2), (4096, 2048, 512, 2)]])
 def test_noalloc_combination_matches_allocating_entry_point(oracle, shapes):
     from volta_mi355x import FP2, Backend
     with Backend() as b:
@@ -59,11 +62,14 @@ def test_noalloc_combination_matches_allocating_entry_point(oracle, shapes):
 
 
 def test_noalloc_combination_refuses_plans_beyond_its_scratch():
-    """2^17 rows of 2048 columns split into 256 partial chunks: two
-    combinations need 16 MiB of partials plus their sums, more than the
-    fixed array; the call fails with an error and writes nothing."""
+    """2^17 rows of 2048 columns in two partial chunks of 2^16 rows (the
+    largest the sums stay exact in): 257 combinations need 2 x 257 x 2048
+    Fp2 partials, just over the fixed 16 MiB array; the call fails with an
+    error and writes nothing.  (At 512-row chunks, 2^17 rows and two
+    combinations also outgrow the array; that plan runs with larger chunks,
+    checked above.)"""
     from volta_mi355x import FP2, Backend
-    rows, cols, comb = 1 << 17, 2048, 2
+    rows, cols, comb = 1 << 17, 2048, 257
     with Backend() as b:
         dw = b.alloc_device(rows * cols, np.int16)
         dp = b.alloc_device(1, np.uint64)

@@ -58,8 +58,9 @@ int pcs_combine_rows(Context* c, const int16_t* w, const uint64_t* pads, const g
                      size_t cols, size_t pad, size_t combinations, gl::Fp2* out);
 // The same combination over dense u64 (Fp) rows.
 // The same combination with its partials and coefficient sums in a fixed
-// device array of COMBINE_SCRATCH_BYTES (no allocation); fails with a clear
-// error when the plan needs more.  combine_scratch_attach resolves the
+// device array of COMBINE_SCRATCH_BYTES (no allocation), with larger row
+// chunks when the usual ones need more; fails with a clear error when even
+// chunks of 2^16 rows need more.  combine_scratch_attach resolves the
 // array's address on the context's device (called by volta_cuda_create).
 constexpr size_t COMBINE_SCRATCH_BYTES = size_t{16} << 20;
 int pcs_combine_rows_noalloc(Context* c, const int16_t* w, const uint64_t* pads, const gl::Fp2* coeffs, size_t rows,

@@ -404,10 +404,16 @@ struct CombinePlan {
     size_t msg_len, col_blocks, chunk, chunks, per_chunk, part_bytes, sum_bytes;
 };
 
-static int combine_plan(Context* c, size_t rows, size_t cols, size_t pad, size_t combinations, CombinePlan* p) {
+// Rows per chunk at most: each wave's u64 accumulators, and each chunk's
+// coefficient half-sums, stay exact up to 2^16 rows.
+constexpr size_t CI_CHUNK_MAX = size_t{1} << 16;
+
+// The plan with comb_chunk's rows per chunk, or `chunk` rows when given.
+static int combine_plan(Context* c, size_t rows, size_t cols, size_t pad, size_t combinations, CombinePlan* p,
+                        size_t chunk = 0) {
     p->msg_len = cols + pad;
     p->col_blocks = (cols + CI_TILE - 1) / CI_TILE;
-    p->chunk = comb_chunk(rows, p->col_blocks, CI_CHUNK);
+    p->chunk = chunk ? chunk : comb_chunk(rows, p->col_blocks, CI_CHUNK);
     p->chunks = (rows + p->chunk - 1) / p->chunk;
     size_t bytes = 0;
     if (!mul_ok(combinations, p->msg_len, &p->per_chunk) || !mul_ok(p->per_chunk * sizeof(Fp2), p->chunks, &bytes) ||
@@ -524,10 +530,16 @@ int pcs_combine_rows_noalloc(Context* c, const int16_t* w, const uint64_t* pads,
         std::string m = "allocation-free PCS combination unavailable on this device: " + c->scratch_error;
         return fail_msg(c, m.c_str());
     }
-    const size_t part_span = (pl.part_bytes + 255) / 256 * 256;
+    auto span = [](const CombinePlan& q) { return (q.part_bytes + 255) / 256 * 256; };
+    // A plan whose partials do not fit the array takes larger row chunks
+    // (fewer partials, the same sums) up to CI_CHUNK_MAX rows per chunk.
+    while (span(pl) + pl.sum_bytes > COMBINE_SCRATCH_BYTES && pl.chunks > 1 && pl.chunk < CI_CHUNK_MAX)
+        if (combine_plan(c, rows, cols, pad, combinations, &pl, std::min(pl.chunk * 2, CI_CHUNK_MAX))) return -1;
+    const size_t part_span = span(pl);
     if (part_span + pl.sum_bytes > COMBINE_SCRATCH_BYTES) {
         std::string m = "allocation-free PCS combination needs " + std::to_string(part_span + pl.sum_bytes) +
-                        " bytes of scratch; its fixed array holds " + std::to_string(COMBINE_SCRATCH_BYTES);
+                        " bytes of scratch at " + std::to_string(CI_CHUNK_MAX) +
+                        " rows per partial chunk; its fixed array holds " + std::to_string(COMBINE_SCRATCH_BYTES);
         return fail_msg(c, m.c_str());
     }
     unsigned char* base = static_cast<unsigned char*>(c->scratch);
