@@ -591,6 +591,28 @@ def test_ntt13_one_pass_host_batch_lengths(backend, oracle, msg_len):
     assert (got == oracle.ntt_forward_batch(padded)).all()
 
 
+@pytest.mark.parametrize("rows,msg_len", [(2063, 2048), (2061, 2049), (300, 8192)])
+def test_host_batch_staged_copies(backend, oracle, rows, msg_len):
+    """Host batches whose copies go through the pinned staging buffers
+    (32 MiB and up: 2,063 x 2,048 and 2,061 x 2,049 inputs of 33.8 MB, their
+    135 MB outputs in 9 chunks of 16 MiB over 8 buffers, the last chunk
+    short; 300 x 8,192 stages only the download).  The caller's arrays are
+    pageable, the input starting 8 bytes into its allocation; every element
+    against the oracle, and the input left as it was."""
+    n = 1 << 13
+    vals = rand_fp(5200 + rows, (rows, msg_len))
+    vals[0, :3] = [0, 1, P - 1]
+    vals[-1, -1] = P - 2
+    buf = np.empty(rows * msg_len + 1, np.uint64)
+    buf[1:] = vals.reshape(-1)
+    host = buf[1:].reshape(rows, msg_len)
+    before = host.copy()
+    got = backend.ntt_fp_batch(host, rows, msg_len, n)
+    assert (host == before).all()
+    assert got.shape == (rows, n)
+    assert (got == oracle.ntt_encode_batch(vals, n)).all()
+
+
 # ---- n = 2^15 in one pass (ntt15.hip) ------------------------------------------------
 
 

@@ -160,13 +160,13 @@ int host_ntt(Context* c, const uint64_t* msgs, size_t rows, size_t msg_len, size
     if (ensure_twiddles(c, n, &h2d, &t)) return -1;
     if (begin_op_h2d(c)) return -1;
     // Compact rows cross PCIe once; zero padding happens in the kernel load.
-    if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<uint64_t>(c, WS_IN), msgs, in_bytes, hipMemcpyHostToDevice, c->stream));
+    if (in_bytes && staged_copy(c, ws<uint64_t>(c, WS_IN), msgs, in_bytes, hipMemcpyHostToDevice)) return -1;
     h2d += in_bytes;
     if (mark_op(c, 1)) return -1;
     if (ntt_fp_rows(c, ws<uint64_t>(c, WS_IN), msg_len, msg_len, rows, n, ws<uint64_t>(c, WS_OUT), t, false))
         return -1;
     if (mark_op(c, 2)) return -1;
-    VMX_HIP(c, hipMemcpyAsync(out, ws<uint64_t>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
+    if (staged_copy(c, out, ws<uint64_t>(c, WS_OUT), bytes, hipMemcpyDeviceToHost)) return -1;
     return finish_op(c, OP_PCS_NTT, h2d, bytes);
 }
 }  // namespace

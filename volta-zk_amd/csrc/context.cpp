@@ -16,6 +16,7 @@
 #include <cstring>
 #include <limits>
 #include <new>
+#include <thread>
 
 #include "gl64.hpp"
 
@@ -189,6 +190,88 @@ int sync_stream(Context* c, SyncReason reason) {
     c->outstanding = 0;
     c->counter_pending = false;
     for (auto& p : c->pinned) p.in_flight = false;
+    return 0;
+}
+
+// ---- host <-> device copies of the host-pointer entry points ---------------------
+// A plain hipMemcpyAsync between pageable host memory and the device moved
+// 4 GiB of codewords at about 18 GB/s and 1 GiB of messages at about 30 GB/s.
+// Staged, thread t of the copy's threads moves chunks t, t + T, t + 2T, ... of
+// STAGE_SLOT_BYTES through its own pinned buffer and event, so the host-side
+// copies of up to T chunks run at once while the DMA engine works through the
+// stream:
+//   download: queue the chunk's DMA into the buffer, wait for its event, copy
+//     the buffer to the caller's memory;
+//   upload: wait for the buffer's previous DMA, copy the caller's chunk into
+//     it, queue its DMA.
+// The threads' DMAs interleave on the one stream, after the work queued before
+// the copy; each thread touches only its own buffer and event.
+
+static bool stage_setup(Context* c) {
+    if (c->stage_ready) return true;
+    for (size_t t = 0; t < c->stage_buf.size(); ++t) {
+        if (!c->stage_buf[t] && hipHostMalloc(&c->stage_buf[t], STAGE_SLOT_BYTES, hipHostMallocDefault) != hipSuccess) {
+            c->stage_buf[t] = nullptr;
+            return false;
+        }
+        if (!c->stage_ev[t]) {
+            // recorded once here, so an upload's first wait on it has a
+            // recorded event to wait for
+            if (hipEventCreateWithFlags(&c->stage_ev[t], hipEventDisableTiming) != hipSuccess) {
+                c->stage_ev[t] = nullptr;
+                return false;
+            }
+            if (hipEventRecord(c->stage_ev[t], c->stream) != hipSuccess) return false;
+        }
+    }
+    c->stage_ready = true;
+    return true;
+}
+
+int staged_copy(Context* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
+    if (kind != hipMemcpyDeviceToHost && kind != hipMemcpyHostToDevice) return fail_msg(c, "staged copy: bad kind");
+    if (bytes < STAGE_MIN_BYTES || !stage_setup(c)) {
+        VMX_HIP(c, hipMemcpyAsync(dst, src, bytes, kind, c->stream));
+        return 0;
+    }
+    const size_t chunks = (bytes + STAGE_SLOT_BYTES - 1) / STAGE_SLOT_BYTES;
+    const size_t threads = std::min(chunks, c->stage_buf.size());
+    const bool down = kind == hipMemcpyDeviceToHost;
+    unsigned char* d = static_cast<unsigned char*>(dst);
+    const unsigned char* s = static_cast<const unsigned char*>(src);
+    std::vector<hipError_t> err(threads, hipSuccess);
+    auto work = [&](size_t t) {
+        hipError_t e = hipSuccess;
+        void* buf = c->stage_buf[t];
+        hipEvent_t ev = c->stage_ev[t];
+        for (size_t k = t; k < chunks && e == hipSuccess; k += threads) {
+            const size_t off = k * STAGE_SLOT_BYTES, len = std::min(STAGE_SLOT_BYTES, bytes - off);
+            if (down) {
+                e = hipMemcpyAsync(buf, s + off, len, hipMemcpyDeviceToHost, c->stream);
+                if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+                if (e == hipSuccess) e = hipEventSynchronize(ev);
+                if (e == hipSuccess) std::memcpy(d + off, buf, len);
+            } else {
+                e = hipEventSynchronize(ev);  // the buffer's previous DMA (none: returns at once)
+                if (e == hipSuccess) std::memcpy(buf, s + off, len);
+                if (e == hipSuccess) e = hipMemcpyAsync(d + off, buf, len, hipMemcpyHostToDevice, c->stream);
+                if (e == hipSuccess) e = hipEventRecord(ev, c->stream);
+            }
+        }
+        err[t] = e;
+    };
+    std::vector<std::thread> pool;
+    pool.reserve(threads - 1);
+    try {
+        for (size_t t = 1; t < threads; ++t) pool.emplace_back(work, t);
+    } catch (...) {
+        for (auto& th : pool) th.join();
+        return fail_msg(c, "staged copy: could not start its threads");
+    }
+    work(0);
+    for (auto& th : pool) th.join();
+    for (hipError_t e : err)
+        if (e != hipSuccess) return fail_hip(c, down ? "staged copy (device to host)" : "staged copy (host to device)", e);
     return 0;
 }
 
@@ -828,6 +911,10 @@ VMX_API void volta_cuda_destroy(void* raw) {
                 if (e) (void)hipEventDestroy(e);
         for (auto e : c->events)
             if (e) (void)hipEventDestroy(e);
+        for (auto e : c->stage_ev)
+            if (e) (void)hipEventDestroy(e);
+        for (void* b : c->stage_buf)
+            if (b) (void)hipHostFree(b);
         if (c->stream) (void)hipStreamDestroy(c->stream);
     } catch (...) {
     }

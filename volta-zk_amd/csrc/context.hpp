@@ -279,6 +279,12 @@ struct Context {
     bool has_pending = false;
     PendingMessages pending{};
     bool bypass_settle = false;
+    // Pinned staging of the host-pointer transforms' large copies
+    // (staged_copy): one buffer and one event per copy thread, allocated on
+    // first use and kept for the context's life.
+    std::array<void*, 8> stage_buf{};
+    std::array<hipEvent_t, 8> stage_ev{};
+    bool stage_ready = false;
     std::string error;
 };
 
@@ -323,6 +329,17 @@ int settle_pending(Context* c);
 // Records that buffer `id` holds message rows the library wrote (Resident::msg_rows);
 // nothing is recorded for a buffer whose address the caller holds.
 void note_message_rows(Context* c, uint64_t id, size_t off, size_t rows, size_t row_len, size_t nonzero);
+
+// ---- host <-> device copies of the host-pointer entry points ---------------------
+// A copy of `bytes` between pageable host memory and the device, on the
+// context's stream after the work queued before it; returns once the data is
+// on the host (download) or queued for the device (upload: the source may be
+// reused at once).  Copies of at least STAGE_MIN_BYTES go through the pinned
+// staging buffers, the rest (or all, if the buffers cannot be pinned) as one
+// hipMemcpyAsync.
+constexpr size_t STAGE_SLOT_BYTES = size_t{16} << 20;
+constexpr size_t STAGE_MIN_BYTES = size_t{32} << 20;
+int staged_copy(Context* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind);
 
 // ---- workspaces and twiddles ---------------------------------------------------
 int ensure_ws(Context* c, int slot, size_t bytes);
