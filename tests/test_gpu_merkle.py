@@ -148,3 +148,11 @@ def test_c3_encoded_matrix_tree_sampled(backend, oracle):
     dm = backend.chacha8_prover_secret_fp_rows_device(bytes([7] * 32), 0, rows, cols)
     _sampled_tree_check(backend, oracle, dm, rows, cols, [0, 1, 4095, 8191])
     backend.free_device(dm)
+
+
+def test_host_column_hashes_staged_upload(backend, oracle):
+    """volta_cuda_hash_fp_columns on a 64 MiB host matrix (8192 rows of 1024
+    columns): its upload goes through the pinned staging buffers."""
+    rows, cols = 8192, 1024
+    m = np.random.Generator(np.random.PCG64(9300)).integers(0, P, size=rows * cols, dtype=np.uint64)
+    assert (backend.hash_fp_columns(m, rows, cols) == oracle.hash_fp_columns(m, rows, cols)).all()

@@ -540,3 +540,33 @@ def test_opening_helper_errors(backend):
     assert "geometry" in backend.last_error()
     assert lib.volta_cuda_logup_eq_rows_device(raw, a.id, 0, 1, 8, a.id, 0) != 0  # 256 outputs > 64 slots
     backend.free_device(a)
+
+
+# ---- host-pointer calls whose copies take the pinned staging (32 MiB and up) ----------
+
+def test_resident_round_trip_staged(backend):
+    """A 40 MiB + 8 B upload and download through the resident buffer API at
+    an element offset: both copies go through the pinned staging buffers
+    (three chunks, the last short); the download equals what was uploaded,
+    and the words around the region are untouched."""
+    n, off = (40 << 20) // 8 + 1, 3
+    data = rand_fp(9100, n)
+    d = backend.alloc_device(n + off + 2, np.uint64)
+    backend.zero_device(d, 0, n + off + 2)
+    backend.upload_into(d, off, data)
+    back = backend.download_device(d, off, n)
+    edges = backend.download_device(d, 0, n + off + 2)
+    backend.free_device(d)
+    assert (back == data).all()
+    assert not edges[:off].any() and not edges[off + n:].any()
+
+
+def test_host_combination_staged_upload(backend, oracle):
+    """The host row combination (volta_cuda_pcs_combine_rows) with 64 MiB of
+    i16 weights and pads: the weights' upload goes through the staging."""
+    rows, cols, pad, comb = 16384, 2048, 8, 2
+    w = rand_i16(9200, rows * cols)
+    pads = rand_fp(9201, rows * pad)
+    co = rand_fp(9202, (comb * rows, 2))
+    got = backend.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)
+    assert (got == oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)).all()

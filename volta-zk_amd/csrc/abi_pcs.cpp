@@ -197,13 +197,13 @@ VMX_API int volta_cuda_ntt_fp2(void* raw, const Fp2* msg, size_t msg_len, size_t
         TwiddleSet* t = nullptr;
         if (ensure_twiddles(c, n, &h2d, &t)) return -1;
         if (begin_op_h2d(c)) return -1;
-        if (in_bytes) VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), msg, in_bytes, hipMemcpyHostToDevice, c->stream));
+        if (in_bytes && staged_copy(c, ws<Fp2>(c, WS_IN), msg, in_bytes, hipMemcpyHostToDevice)) return -1;
         if (bytes > in_bytes && zero_bytes(c, ws<unsigned char>(c, WS_IN) + in_bytes, bytes - in_bytes)) return -1;
         h2d += bytes;
         if (mark_op(c, 1)) return -1;
         if (ntt_fp2_rows(c, ws<uint64_t>(c, WS_IN), 1, n, ws<uint64_t>(c, WS_OUT), t)) return -1;
         if (mark_op(c, 2)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(out, ws<Fp2>(c, WS_OUT), bytes, hipMemcpyDeviceToHost, c->stream));
+        if (staged_copy(c, out, ws<Fp2>(c, WS_OUT), bytes, hipMemcpyDeviceToHost)) return -1;
         return finish_op(c, OP_PCS_NTT, h2d, bytes);
     });
 }
@@ -338,15 +338,16 @@ VMX_API int volta_cuda_pcs_combine_rows(void* raw, const int16_t* weights, const
             ensure_ws(c, WS_OUT, ob))
             return -1;
         if (begin_op_h2d(c)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), weights, wb, hipMemcpyHostToDevice, c->stream));
-        if (pb) VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), pads, pb, hipMemcpyHostToDevice, c->stream));
-        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX1), coeffs, cb, hipMemcpyHostToDevice, c->stream));
+        if (staged_copy(c, ws<void>(c, WS_IN), weights, wb, hipMemcpyHostToDevice) ||
+            (pb && staged_copy(c, ws<void>(c, WS_AUX0), pads, pb, hipMemcpyHostToDevice)) ||
+            staged_copy(c, ws<void>(c, WS_AUX1), coeffs, cb, hipMemcpyHostToDevice))
+            return -1;
         if (mark_op(c, 1)) return -1;
         if (pcs_combine_rows(c, ws<int16_t>(c, WS_IN), ws<uint64_t>(c, WS_AUX0), ws<Fp2>(c, WS_AUX1), rows, cols, pad,
                              combinations, ws<Fp2>(c, WS_OUT)))
             return -1;
         if (mark_op(c, 2)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost, c->stream));
+        if (staged_copy(c, out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost)) return -1;
         return finish_op(c, OP_PCS_ROWS, wb + pb + cb, ob);
     });
 }
@@ -423,14 +424,15 @@ VMX_API int volta_cuda_pcs_gather_columns(void* raw, const uint64_t* matrix, siz
         const size_t ib = queries * 4;
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_AUX0, ib) || ensure_ws(c, WS_OUT, ob)) return -1;
         if (begin_op_h2d(c)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
-        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_AUX0), idx, ib, hipMemcpyHostToDevice, c->stream));
+        if (staged_copy(c, ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice) ||
+            staged_copy(c, ws<void>(c, WS_AUX0), idx, ib, hipMemcpyHostToDevice))
+            return -1;
         if (mark_op(c, 1)) return -1;
         if (gather_columns(c, ws<uint64_t>(c, WS_IN), ws<uint32_t>(c, WS_AUX0), ws<uint64_t>(c, WS_OUT), rows, cols,
                            queries, false))
             return -1;
         if (mark_op(c, 2)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost, c->stream));
+        if (staged_copy(c, out, ws<void>(c, WS_OUT), ob, hipMemcpyDeviceToHost)) return -1;
         return finish_op(c, OP_PCS_ROWS, mb + ib, ob);
     });
 }
@@ -780,7 +782,7 @@ VMX_API int volta_cuda_hash_fp_columns(void* raw, const uint64_t* matrix, size_t
             return fail_msg(c, "PCS hash matrix geometry overflows size_t");
         if (ensure_ws(c, WS_IN, mb) || ensure_ws(c, WS_OUT, hb)) return -1;
         if (begin_op_h2d(c)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice, c->stream));
+        if (staged_copy(c, ws<void>(c, WS_IN), matrix, mb, hipMemcpyHostToDevice)) return -1;
         if (mark_op(c, 1)) return -1;
         if (merkle_column_leaves(c, ws<uint64_t>(c, WS_IN), rows, cols, false, ws<uint32_t>(c, WS_OUT))) return -1;
         if (mark_op(c, 2)) return -1;
@@ -892,12 +894,12 @@ VMX_API int volta_cuda_x4b_ntt_fp2(void* raw, const Fp2* coefficients, size_t co
         X4Tables tb;
         if (x4_tables(c, log2_of(n), &h2d, &tb)) return -1;
         if (begin_op_h2d(c)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(ws<Fp2>(c, WS_IN), coefficients, in_bytes, hipMemcpyHostToDevice, c->stream));
+        if (staged_copy(c, ws<Fp2>(c, WS_IN), coefficients, in_bytes, hipMemcpyHostToDevice)) return -1;
         h2d += in_bytes;
         if (mark_op(c, 1)) return -1;
         if (x4_ntt(c, tb, ws<Fp2>(c, WS_IN), coefficient_len, ws<Fp2>(c, WS_OUT))) return -1;
         if (mark_op(c, 2)) return -1;
-        VMX_HIP(c, hipMemcpyAsync(output, ws<Fp2>(c, WS_OUT), total, hipMemcpyDeviceToHost, c->stream));
+        if (staged_copy(c, output, ws<Fp2>(c, WS_OUT), total, hipMemcpyDeviceToHost)) return -1;
         return finish_op(c, OP_PCS_NTT, h2d, total, 0, total - in_bytes);
     });
 }

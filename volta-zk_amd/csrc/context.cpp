@@ -1231,9 +1231,9 @@ VMX_API int volta_cuda_resident_upload(void* raw, uint64_t id, size_t off, const
     if (region(c, id, off, bytes, &dst)) return -1;
     if (begin_transfer(c)) return -1;
     const auto t0 = std::chrono::steady_clock::now();
-    const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream);
+    const int rc = staged_copy(c, dst, src, bytes, hipMemcpyHostToDevice);
     const auto t1 = std::chrono::steady_clock::now();
-    if (e != hipSuccess) return fail_hip(c, "hipMemcpyAsync(resident H2D)", e);
+    if (rc) return -1;
     ++c->stats.resident_h2d_host_calls;
     c->stats.resident_h2d_host_call_ns += std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
     return finish_transfer(c, bytes, true);
@@ -1246,9 +1246,9 @@ VMX_API int volta_cuda_resident_download(void* raw, uint64_t id, size_t off, voi
     if (region(c, id, off, bytes, &src, true)) return -1;
     if (begin_transfer(c)) return -1;
     const auto t0 = std::chrono::steady_clock::now();
-    const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream);
+    const int rc = staged_copy(c, dst, src, bytes, hipMemcpyDeviceToHost);
     const auto t1 = std::chrono::steady_clock::now();
-    if (e != hipSuccess) return fail_hip(c, "hipMemcpyAsync(resident D2H)", e);
+    if (rc) return -1;
     ++c->stats.resident_d2h_host_calls;
     c->stats.resident_d2h_host_call_ns += std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
     return finish_transfer(c, bytes, false);
