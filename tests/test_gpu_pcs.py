@@ -570,3 +570,35 @@ def test_host_combination_staged_upload(backend, oracle):
     co = rand_fp(9202, (comb * rows, 2))
     got = backend.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)
     assert (got == oracle.pcs_combine_rows(w, pads, co, rows, cols, pad, comb)).all()
+
+
+def test_resident_round_trip_from_pinned_host_memory(backend):
+    """A 40 MiB upload and download whose host buffers the caller pinned
+    (hipHostMalloc from the HIP runtime the library uses): copied directly,
+    no staging; the download equals the upload, and a launch after the copies
+    reports no stale error."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    n = (40 << 20) // 8
+    ptrs = [ctypes.c_void_p(), ctypes.c_void_p()]
+    for q in ptrs:
+        assert hip.hipHostMalloc(ctypes.byref(q), n * 8, 0) == 0
+    try:
+        src = np.ctypeslib.as_array((ctypes.c_uint64 * n).from_address(ptrs[0].value))
+        dst = np.ctypeslib.as_array((ctypes.c_uint64 * n).from_address(ptrs[1].value))
+        src[:] = rand_fp(9400, n)
+        dst[:] = 0
+        d = backend.alloc_device(n, np.uint64)
+        assert backend.lib.volta_cuda_resident_upload(backend.raw, d.id, 0, ptrs[0].value, n * 8) == 0, \
+            backend.last_error()
+        assert backend.lib.volta_cuda_resident_download(backend.raw, d.id, 0, ptrs[1].value, n * 8) == 0, \
+            backend.last_error()
+        assert (src == dst).all()
+        out = backend.ntt_fp_batch_device(d, 1 << 10, 1 << 12)  # launches after the copies
+        backend.free_device(out)
+        backend.free_device(d)
+    finally:
+        for q in ptrs:
+            hip.hipHostFree(q)

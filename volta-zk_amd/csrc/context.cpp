@@ -230,7 +230,18 @@ static bool stage_setup(Context* c) {
 
 int staged_copy(Context* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
     if (kind != hipMemcpyDeviceToHost && kind != hipMemcpyHostToDevice) return fail_msg(c, "staged copy: bad kind");
-    if (bytes < STAGE_MIN_BYTES || !stage_setup(c)) {
+    // A host buffer the caller pinned needs no staging.  For pageable memory
+    // the query fails (hipErrorInvalidValue); its error is cleared at once so
+    // that no later hipGetLastError reports it.
+    bool pinned = false;
+    if (bytes >= STAGE_MIN_BYTES) {
+        hipPointerAttribute_t attr{};
+        if (hipPointerGetAttributes(&attr, kind == hipMemcpyDeviceToHost ? dst : src) == hipSuccess)
+            pinned = attr.type == hipMemoryTypeHost;
+        else
+            (void)hipGetLastError();
+    }
+    if (bytes < STAGE_MIN_BYTES || pinned || !stage_setup(c)) {
         VMX_HIP(c, hipMemcpyAsync(dst, src, bytes, kind, c->stream));
         return 0;
     }

@@ -334,8 +334,9 @@ void note_message_rows(Context* c, uint64_t id, size_t off, size_t rows, size_t 
 // A copy of `bytes` between pageable host memory and the device, on the
 // context's stream after the work queued before it; returns once the data is
 // on the host (download) or queued for the device (upload: the source may be
-// reused at once).  Copies of at least STAGE_MIN_BYTES go through the pinned
-// staging buffers, the rest (or all, if the buffers cannot be pinned) as one
+// reused at once).  Copies of at least STAGE_MIN_BYTES of pageable host memory
+// go through the pinned staging buffers; the rest, copies of host memory the
+// caller pinned, and all copies if the buffers cannot be pinned are one
 // hipMemcpyAsync.
 constexpr size_t STAGE_SLOT_BYTES = size_t{16} << 20;
 constexpr size_t STAGE_MIN_BYTES = size_t{32} << 20;
