@@ -23,24 +23,65 @@ static unsigned grid_for(size_t items, size_t per_block, size_t cap = 1u << 20) 
 }
 
 // ---- message rows (reference pcs_messages_kernel, .cu:2950-2958) --------------------
+// A workgroup writes one span of MSG_THREADS x MSG_PER consecutive elements in
+// each of the rows it walks: block b takes span b mod S of rows
+// b / S, b / S + G, ... (S spans per row, G = gridDim.x / S), so the division
+// happens once per workgroup and none per element; each store instruction
+// writes 512 contiguous bytes, non-temporal (the rows are larger than the
+// caches).  8-byte stores: the output may start at any element offset.
+constexpr int MSG_THREADS = 256, MSG_PER = 8;
 
-__global__ void messages_kernel(const int16_t* w, const uint64_t* pads, uint64_t* out, size_t rows, size_t cols,
-                                size_t pad, size_t code_len) {
-    const size_t total = rows * code_len;
-    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
-    for (size_t z = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; z < total; z += stride) {
-        const size_t r = z / code_len, j = z - r * code_len;
-        uint64_t v = 0;
-        if (j < cols) v = gl::from_i16(w[r * cols + j]);
-        else if (j < cols + pad) v = pads[r * pad + (j - cols)];
-        out[z] = v;
+__global__ __launch_bounds__(MSG_THREADS) void messages_kernel(const int16_t* w, const uint64_t* pads, uint64_t* out,
+                                                               size_t rows, size_t cols, size_t pad, size_t code_len,
+                                                               unsigned spans_per_row) {
+    constexpr size_t SPAN = size_t{MSG_THREADS} * MSG_PER;
+    const unsigned row_step = gridDim.x / spans_per_row;
+    const unsigned r0 = blockIdx.x / spans_per_row;
+    const size_t j0 = static_cast<size_t>(blockIdx.x - r0 * spans_per_row) * SPAN;
+    // the span's kind is uniform over the workgroup: all zero tail, all
+    // weights, or mixed
+    const bool zeros = j0 >= cols + pad, weights = j0 + SPAN <= cols;
+    for (size_t r = r0; r < rows; r += row_step) {
+        const int16_t* wr = w + r * cols;
+        uint64_t* o = out + r * code_len;
+        if (zeros) {
+#pragma unroll
+            for (int k = 0; k < MSG_PER; ++k) {
+                const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
+                if (j < code_len) __builtin_nontemporal_store(uint64_t{0}, o + j);
+            }
+        } else if (weights) {
+#pragma unroll
+            for (int k = 0; k < MSG_PER; ++k) {
+                const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
+                __builtin_nontemporal_store(gl::from_i16(wr[j]), o + j);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < MSG_PER; ++k) {
+                const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
+                if (j < code_len) {
+                    uint64_t v = 0;
+                    if (j < cols) v = gl::from_i16(wr[j]);
+                    else if (j < cols + pad) v = pads[r * pad + (j - cols)];
+                    __builtin_nontemporal_store(v, o + j);
+                }
+            }
+        }
     }
 }
 
 int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows, size_t cols, size_t pad,
                  size_t code_len, uint64_t* out) {
-    hipLaunchKernelGGL(messages_kernel, dim3(grid_for(rows * code_len, 256)), dim3(256), 0, c->stream, w, pads,
-                       out, rows, cols, pad, code_len);
+    constexpr size_t SPAN = size_t{MSG_THREADS} * MSG_PER;
+    const size_t spans = (code_len + SPAN - 1) / SPAN;
+    if (spans > (1u << 20)) return fail_msg(c, "message row too long for the message kernel");
+    const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
+    // rows per span column: enough workgroups for about 64 per CU, at most one per row
+    const size_t row_groups = std::max<size_t>(1, std::min(rows, std::max<size_t>(1, cus * 64 / spans)));
+    const unsigned blocks = static_cast<unsigned>(spans * row_groups);
+    hipLaunchKernelGGL(messages_kernel, dim3(blocks), dim3(MSG_THREADS), 0, c->stream, w, pads, out, rows, cols, pad,
+                       code_len, static_cast<unsigned>(spans));
     VMX_HIP(c, hipGetLastError());
     return 0;
 }
