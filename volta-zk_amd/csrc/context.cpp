@@ -252,7 +252,8 @@ int staged_copy(Context* c, void* dst, const void* src, size_t bytes, hipMemcpyK
     const unsigned char* s = static_cast<const unsigned char*>(src);
     std::vector<hipError_t> err(threads, hipSuccess);
     auto work = [&](size_t t) {
-        hipError_t e = hipSuccess;
+        // a new thread's current device is the default one: use the context's
+        hipError_t e = t ? hipSetDevice(c->device) : hipSuccess;
         void* buf = c->stage_buf[t];
         hipEvent_t ev = c->stage_ev[t];
         for (size_t k = t; k < chunks && e == hipSuccess; k += threads) {
