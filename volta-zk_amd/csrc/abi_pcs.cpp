@@ -232,7 +232,6 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
             c->pending.rows * c->pending.code_len == on)
             c->has_pending = false;
         if (region_elems(c, out_id, out_off, on, 8, &out)) return -1;
-        if (begin_op(c) || mark_op(c, 1)) return -1;
         // The rows are recorded, not written, when their buffer is separate
         // from the sources: a following forward NTT of exactly these rows
         // (finish_resident_commit, rust/volta-pcs/src/ligero.rs:477-496) then
@@ -241,14 +240,25 @@ VMX_API int volta_cuda_pcs_messages_device(void* raw, uint64_t w_id, size_t w_of
         // the caller holds the device address of the rows' buffer or of a
         // source (volta_mi355x_resident_device_ptr), since its own kernels
         // could read the rows or change a source behind the library.  The
-        // stats are those of a messages call either way.
+        // stats are those of a messages call either way; a call that only
+        // records its rows runs nothing on the device and so has no timing
+        // record of its own (its kernel time is the later write's, or the
+        // fused encode's).
         const bool exposed = find_resident(c, out_id)->exposed || find_resident(c, w_id)->exposed ||
                              (pad && find_resident(c, pads_id)->exposed);
-        if (!exposed && out_id != w_id && (!pad || out_id != pads_id)) {
-            if (c->has_pending && settle_pending(c)) return -1;  // one record at a time
-            c->pending = PendingMessages{out_id, out_off, static_cast<uint64_t*>(out), w_id, pad ? pads_id : 0,
-                                         static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
-                                         rows, cols, pad, code_len};
+        const bool defer = !exposed && out_id != w_id && (!pad || out_id != pads_id);
+        const PendingMessages rec{out_id, out_off, static_cast<uint64_t*>(out), w_id, pad ? pads_id : 0,
+                                  static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads),
+                                  rows, cols, pad, code_len};
+        if (defer && !c->has_pending) {
+            c->pending = rec;
+            c->has_pending = true;
+            return empty_op(c, OP_PCS_ROWS);
+        }
+        if (begin_op(c) || mark_op(c, 1)) return -1;
+        if (defer) {
+            if (settle_pending(c)) return -1;  // one record at a time
+            c->pending = rec;
             c->has_pending = true;
         } else {
             if (pcs_messages(c, static_cast<const int16_t*>(w), static_cast<const uint64_t*>(pads), rows, cols, pad,
@@ -647,6 +657,7 @@ VMX_API int volta_mi355x_probe_copy_device(void* raw, uint64_t src_id, uint64_t 
     if (!c || !bytes || bytes % 16) return fail_msg(c, "invalid copy probe geometry (bytes must be a multiple of 16)");
     void *s = nullptr, *d = nullptr;
     if (region(c, src_id, 0, bytes, &s, true) || region(c, dst_id, 0, bytes, &d)) return -1;
+    stream_touched(c);  // no timing record: outside any primitive's markers
     return probe_copy(c, s, d, bytes);
 }
 
@@ -657,6 +668,7 @@ VMX_API int volta_mi355x_probe_expand_device(void* raw, uint64_t src_id, uint64_
     if (!mul_ok(src_bytes, 16, &dst_bytes)) return fail_msg(c, "expand probe geometry overflows size_t");
     void *s = nullptr, *d = nullptr;
     if (region(c, src_id, 0, src_bytes, &s, true) || region(c, dst_id, 0, dst_bytes, &d)) return -1;
+    stream_touched(c);  // no timing record: outside any primitive's markers
     return probe_expand(c, s, d, src_bytes);
 }
 
@@ -668,6 +680,7 @@ VMX_API int volta_mi355x_probe_fp2_device(void* raw, uint64_t a_id, uint64_t b_i
     if (region_elems(c, a_id, 0, n, 16, &a, true) || region_elems(c, b_id, 0, n, 16, &b, true) ||
         region_elems(c, out_id, 0, n, 16, &o))
         return -1;
+    stream_touched(c);  // no timing record: outside any primitive's markers
     if (rounds == 0)
         return probe_fp2_stream(c, static_cast<const Fp2*>(a), static_cast<const Fp2*>(b), static_cast<Fp2*>(o), n);
     return probe_fp2_chain(c, static_cast<const Fp2*>(a), static_cast<const Fp2*>(b), static_cast<Fp2*>(o), n, rounds);

@@ -190,6 +190,7 @@ int sync_stream(Context* c, SyncReason reason) {
     c->outstanding = 0;
     c->counter_pending = false;
     for (auto& p : c->pinned) p.in_flight = false;
+    stream_touched(c);
     return 0;
 }
 
@@ -230,6 +231,7 @@ static bool stage_setup(Context* c) {
 
 int staged_copy(Context* c, void* dst, const void* src, size_t bytes, hipMemcpyKind kind) {
     if (kind != hipMemcpyDeviceToHost && kind != hipMemcpyHostToDevice) return fail_msg(c, "staged copy: bad kind");
+    stream_touched(c);
     // A host buffer the caller pinned needs no staging.  For pageable memory
     // the query fails (hipErrorInvalidValue); its error is cleared at once so
     // that no later hipGetLastError reports it.
@@ -346,7 +348,10 @@ int ensure_twiddles(Context* c, size_t n, uint64_t* h2d, TwiddleSet** out) {
         if (upload_table(c, host, &t.fwd, h2d)) return -1;
     }
     // the pass engine's tables come from fwd on the device: no further H2D
-    if (!t.reg && n <= (size_t{1} << 31) && reg_ntt_covers(n) && derive_reg_tables(c, &t)) return -1;
+    if (!t.reg && n <= (size_t{1} << 31) && reg_ntt_covers(n)) {
+        stream_touched(c);  // the tables' kernels run outside any primitive's markers
+        if (derive_reg_tables(c, &t)) return -1;
+    }
     *out = &t;
     return 0;
 }
@@ -425,6 +430,7 @@ static hipError_t ev_create(Context* c, hipEvent_t* e) {
 
 static hipError_t ev_record(Context* c, hipEvent_t e) {
     ++c->stats.timing_event_api_calls;
+    stream_touched(c);
     return hipEventRecord(e, c->stream);
 }
 
@@ -470,6 +476,7 @@ static int ring_take(Context* c, size_t* slot) {
     for (auto& e : r.ev)
         if (!e) VMX_HIP(c, ev_create(c, &e));
     r.mask = 0;
+    r.start = nullptr;
     r.op = -1;
     r.coarse = r.transfer_h2d = r.transfer_d2h = false;
     r.h2d = r.d2h = r.d2d = r.zeroed = r.generated = 0;
@@ -502,7 +509,7 @@ int flush_deferred(Context* c, SyncReason reason) {
                 if (ev_ns(c, r.ev[0], r.ev[1], &ns)) return -1;
                 c->stats.h2d_ns += ns;
             }
-            if (ev_ns(c, r.ev[1], r.ev[2], &ns)) return -1;
+            if (ev_ns(c, r.start ? r.start : r.ev[1], r.ev[2], &ns)) return -1;
             c->stats.kernel_ns[r.op] += ns;
             if (r.d2h) {
                 if (ev_ns(c, r.ev[2], r.ev[3], &ns)) return -1;
@@ -561,17 +568,51 @@ int begin_op_h2d(Context* c) {
     return 0;
 }
 
+// Marker 1 of a device-only record can be the previous record's marker 2 when
+// that marker is still the last thing enqueued on the stream and the device
+// has not reached it: the kernels that follow then start as soon as it
+// completes, exactly as they would after a marker of their own, and the stream
+// runs one marker fewer.  Each marker costs the device about 3 us between
+// kernels on this runtime (the next dispatch is only processed after it), a
+// third of a small configuration's step.  A marker the device has already
+// passed is not borrowed: the stream may have gone idle since, and that gap is
+// no kernel's time.  The window between this query and the next launch is the
+// only slack (host microseconds, and only when the device catches up within it).
+static int borrow_start(Context* c, TimingRecord* r) {
+    const long prev = c->reuse_slot;
+    c->reuse_slot = -1;
+    if (prev < 0) return 0;
+    hipEvent_t e = c->ring[static_cast<size_t>(prev)].ev[2];
+    ++c->stats.timing_event_api_calls;
+    const hipError_t q = hipEventQuery(e);
+    if (q == hipSuccess) return 0;
+    if (q != hipErrorNotReady) return fail_hip(c, "hipEventQuery", q);
+    (void)hipGetLastError();  // not-ready is a state: keep it out of the next launch check
+    r->start = e;
+    return 1;
+}
+
 int mark_op(Context* c, int which) {
     if (which != 1 && which != 2) return fail_msg(c, "invalid timing marker");
     if (c->coarse_active) return c->coarse_inner ? 0 : fail_msg(c, "coarse marker without primitive");
     switch (c->timing_mode) {
         case TIMING_WALL_ONLY_COUNTERS:
             return c->counter_active ? 0 : fail_msg(c, "counter marker without primitive");
-        case TIMING_EVENTS_DEFERRED:
+        case TIMING_EVENTS_DEFERRED: {
             if (!c->record_active) return fail_msg(c, "deferred marker without record");
-            VMX_HIP(c, ev_record(c, c->ring[c->active_slot].ev[which]));
-            c->ring[c->active_slot].mask |= static_cast<uint8_t>(1u << which);
+            TimingRecord& r = c->ring[c->active_slot];
+            if (which == 1 && !(r.mask & 1)) {
+                const int shared = borrow_start(c, &r);
+                if (shared < 0) return -1;
+                if (shared) {
+                    r.mask |= 2;
+                    return 0;
+                }
+            }
+            VMX_HIP(c, ev_record(c, r.ev[which]));
+            r.mask |= static_cast<uint8_t>(1u << which);
             return 0;
+        }
         case TIMING_EVENTS:
             VMX_HIP(c, ev_record(c, c->events[which]));
             return 0;
@@ -635,6 +676,8 @@ int finish_op(Context* c, int op, uint64_t h2d, uint64_t d2h, uint64_t d2d, uint
             r.h2d = (r.mask & 1) ? h2d : 0;
             r.d2h = d2h;
             ring_commit(c);
+            // marker 2 is the stream's last item unless a download followed it
+            if (!d2h && (r.mask & 4)) c->reuse_slot = static_cast<long>(c->active_slot);
             account(c, op, h2d, d2h, d2d, zeroed, generated);
             return d2h ? flush_deferred(c, SyncReason::HostOutput) : 0;
         }
@@ -672,6 +715,15 @@ int finish_op(Context* c, int op, uint64_t h2d, uint64_t d2h, uint64_t d2d, uint
             return 0;
         }
     }
+}
+
+int empty_op(Context* c, int op) {
+    if (c->timing_mode != TIMING_EVENTS_DEFERRED || c->coarse_active)
+        return (begin_op(c) || mark_op(c, 1) || mark_op(c, 2)) ? -1 : finish_op(c, op, 0, 0);
+    if (c->record_active) return fail_msg(c, "empty primitive inside a timing record");
+    ++c->outstanding;
+    account(c, op, 0, 0, 0, 0, 0);
+    return 0;
 }
 
 int begin_transfer(Context* c) {
@@ -834,6 +886,7 @@ int pinned_ready(Context* c, Pinned* p, bool* ready) {
 
 int pinned_mark_in_flight(Context* c, Pinned* p) {
     if (!p->ready) return fail_msg(c, "pinned buffer has no ready event");
+    stream_touched(c);
     VMX_HIP(c, hipEventRecord(p->ready, c->stream));
     p->in_flight = true;
     return 0;
@@ -1279,6 +1332,7 @@ __global__ void vmx_zero_kernel(uint4* dst, size_t n16, unsigned char* tail, siz
 namespace vmx {
 // Zero `bytes` at `dst` on the context stream.
 int zero_bytes(Context* c, void* dst, size_t bytes) {
+    stream_touched(c);
     unsigned char* p = static_cast<unsigned char*>(dst);
     // Leading bytes until 16-byte alignment, handled with the tail path.
     size_t head = (16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15;

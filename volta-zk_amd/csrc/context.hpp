@@ -183,8 +183,10 @@ enum WorkspaceSlot : int {
 
 struct TimingRecord {
     hipEvent_t ev[4]{};
+    // marker 1 borrowed from the previous record's marker 2 (null: ev[1])
+    hipEvent_t start = nullptr;
     int op = -1;
-    uint8_t mask = 0;  // which of ev[] were recorded
+    uint8_t mask = 0;  // which of ev[] were recorded (bit 1 also when marker 1 is borrowed)
     bool coarse = false;
     bool transfer_h2d = false;
     bool transfer_d2h = false;
@@ -253,6 +255,10 @@ struct Context {
     size_t ring_pending = 0;
     bool record_active = false;  // a ring/legacy record is between begin and finish
     size_t active_slot = 0;
+    // The ring slot whose marker 2 is the last thing enqueued on the stream
+    // (-1: none, or other work followed it); the next device-only record may
+    // open with that marker instead of recording its own.
+    long reuse_slot = -1;
     // coarse scopes
     bool coarse_active = false;
     bool coarse_inner = false;
@@ -373,5 +379,11 @@ int begin_transfer(Context* c);
 int finish_transfer(Context* c, size_t bytes, bool h2d);
 int sync_stream(Context* c, SyncReason reason);
 int flush_deferred(Context* c, SyncReason reason);
+// A primitive that enqueues nothing on the device: counted as a call, with no
+// timing record (under deferred events) and so no markers on the stream.
+int empty_op(Context* c, int op);
+// Work enqueued on the stream outside a primitive's markers: the last record's
+// closing marker can no longer open the next one.
+inline void stream_touched(Context* c) { c->reuse_slot = -1; }
 
 }  // namespace vmx
