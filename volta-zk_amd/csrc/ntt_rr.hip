@@ -38,6 +38,16 @@ __global__ __launch_bounds__(Shape<B>::THREADS, Shape<B>::WAVES_PER_SIMD) void r
         asm volatile("" : "+v"(tt));
         return role<B>(tt);
     };
+    // Wave priority by phase.  The four workgroups of a CU run the same phases
+    // out of step; a wave in stage C and its stores goes first (2), then one
+    // loading its next row, running stage A and writing its first exchange
+    // (1), and the waves between barriers in the exchanges and stage B fill
+    // what is left (0).  The loads of the next row so leave early and overlap
+    // the other workgroups' exchanges.  C3-shape rows in full, mostly zero
+    // (the written commit chain): 2.50-2.57 -> 2.15 ms; rows read to 2^11:
+    // 2.29-2.36 -> 2.08 ms.  One priority for the loads and stage A only gave
+    // 2.46-2.49 ms; the same through the whole first exchange 2.22-2.24 ms.
+    __builtin_amdgcn_s_setprio(1);
     for (size_t row = blockIdx.x; row < rows; row += gridDim.x) {
         uint64_t v[32], tw[8];
         load_row<B, NZ>(v, in, stride, len, row, here().m);
@@ -65,6 +75,7 @@ __global__ __launch_bounds__(Shape<B>::THREADS, Shape<B>::WAVES_PER_SIMD) void r
             if (w0 == 0) x1_write<B, 0>(lds, v, tw, t1, q.m);
             else x1_write<B, 1>(lds, v, tw, t1, q.m);
         }
+        __builtin_amdgcn_s_setprio(0);  // the exchanges and stage B yield to the other workgroups
         __builtin_amdgcn_sched_barrier(0);
         load_tw1<B, 0>(tw, t1, w0 ^ 1, here().m);
         __syncthreads();
@@ -102,6 +113,7 @@ __global__ __launch_bounds__(Shape<B>::THREADS, Shape<B>::WAVES_PER_SIMD) void r
             }
             __syncthreads();
         });
+        __builtin_amdgcn_s_setprio(2);
         stage_c<B>(v);
         // X[k3 + 32 (p + P x) + 1024 k1] from slot p + P k1: lane offset
         // (k3 + 32 P x) 8, scalar offset (32 p + 1024 k1) 8, non-temporal (aux bit 1)
@@ -113,6 +125,7 @@ __global__ __launch_bounds__(Shape<B>::THREADS, Shape<B>::WAVES_PER_SIMD) void r
             const v2u d = {static_cast<uint32_t>(v[s]), static_cast<uint32_t>(v[s] >> 32)};
             __builtin_amdgcn_raw_buffer_store_b64(d, orow, qo, (32 * pp + 1024 * k1) * 8u, 2);
         });
+        __builtin_amdgcn_s_setprio(1);  // the next row's loads, stage A and first exchange write
     }
 #endif
 }
