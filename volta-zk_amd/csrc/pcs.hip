@@ -23,12 +23,20 @@ static unsigned grid_for(size_t items, size_t per_block, size_t cap = 1u << 20) 
 }
 
 // ---- message rows (reference pcs_messages_kernel, .cu:2950-2958) --------------------
-// A workgroup writes one span of MSG_THREADS x MSG_PER consecutive elements in
-// each of the rows it walks: block b takes span b mod S of rows
-// b / S, b / S + G, ... (S spans per row, G = gridDim.x / S), so the division
-// happens once per workgroup and none per element; each store instruction
-// writes 512 contiguous bytes, non-temporal (the rows are larger than the
-// caches).  8-byte stores: the output may start at any element offset.
+// A row is cut into S spans of MSG_THREADS x MSG_PER consecutive elements.
+// Workgroup b walks rows r0, r0 + G, r0 + 2G, ... (G = gridDim.x / S row
+// groups, r0 = b / S) and takes span (b + i) mod S of its i-th row, so every
+// (row, span) is written once and each workgroup meets every kind of span in
+// turn: the weight spans, which wait on loads, are spread over all workgroups
+// instead of holding a quarter of them to the end.  The next unit's weights
+// load before the current unit's stores.  The span's kind is uniform over the
+// workgroup (a scalar branch); there is no division per element.  Each store
+// instruction writes 512 contiguous bytes, non-temporal (the rows are larger
+// than the caches).  8-byte stores: the output may start at any element
+// offset.  C3 (2^16 rows of 2^11 weights into 2^13): 1.09 ms with a fixed span
+// per workgroup, 0.91 ms with the rotation, 0.90 ms with the prefetch, 0.845
+// ms at 128 workgroups per CU (64: 0.90, 256: 0.89); the same stores without
+// any loads take 0.80 ms.
 constexpr int MSG_THREADS = 256, MSG_PER = 8;
 
 __global__ __launch_bounds__(MSG_THREADS) void messages_kernel(const int16_t* w, const uint64_t* pads, uint64_t* out,
@@ -36,35 +44,54 @@ __global__ __launch_bounds__(MSG_THREADS) void messages_kernel(const int16_t* w,
                                                                unsigned spans_per_row) {
     constexpr size_t SPAN = size_t{MSG_THREADS} * MSG_PER;
     const unsigned row_step = gridDim.x / spans_per_row;
-    const unsigned r0 = blockIdx.x / spans_per_row;
-    const size_t j0 = static_cast<size_t>(blockIdx.x - r0 * spans_per_row) * SPAN;
-    // the span's kind is uniform over the workgroup: all zero tail, all
-    // weights, or mixed
-    const bool zeros = j0 >= cols + pad, weights = j0 + SPAN <= cols;
-    for (size_t r = r0; r < rows; r += row_step) {
-        const int16_t* wr = w + r * cols;
+    size_t r = blockIdx.x / spans_per_row;
+    unsigned s = blockIdx.x - static_cast<unsigned>(r) * spans_per_row;
+    // 0: all zero tail, 1: all weights, 2: mixed
+    auto kind = [&](unsigned sp) {
+        const size_t j0 = static_cast<size_t>(sp) * SPAN;
+        return j0 >= cols + pad ? 0 : (j0 + SPAN <= cols ? 1 : 2);
+    };
+    auto load_span = [&](size_t row, unsigned sp, int16_t* dst) {
+        const int16_t* src = w + row * cols + static_cast<size_t>(sp) * SPAN + threadIdx.x;
+#pragma unroll
+        for (int k = 0; k < MSG_PER; ++k) dst[k] = src[static_cast<size_t>(k) * MSG_THREADS];
+    };
+    int16_t nxt[MSG_PER];
+    if (r < rows && kind(s) == 1) load_span(r, s, nxt);
+    for (; r < rows; r += row_step, s = (s + 1 == spans_per_row) ? 0 : s + 1) {
+        const size_t j0 = static_cast<size_t>(s) * SPAN;
         uint64_t* o = out + r * code_len;
-        if (zeros) {
+        const int kd = kind(s);
+        int16_t cur[MSG_PER];
+        if (kd == 1) {
+#pragma unroll
+            for (int k = 0; k < MSG_PER; ++k) cur[k] = nxt[k];
+        }
+        const size_t rn = r + row_step;
+        const unsigned sn = (s + 1 == spans_per_row) ? 0 : s + 1;
+        if (rn < rows && kind(sn) == 1) load_span(rn, sn, nxt);
+        if (kd == 0) {
 #pragma unroll
             for (int k = 0; k < MSG_PER; ++k) {
                 const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
                 if (j < code_len) __builtin_nontemporal_store(uint64_t{0}, o + j);
             }
-        } else if (weights) {
+        } else if (kd == 1) {
 #pragma unroll
             for (int k = 0; k < MSG_PER; ++k) {
                 const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
-                __builtin_nontemporal_store(gl::from_i16(wr[j]), o + j);
+                __builtin_nontemporal_store(gl::from_i16(cur[k]), o + j);
             }
         } else {
+            const int16_t* wr = w + r * cols;
 #pragma unroll
             for (int k = 0; k < MSG_PER; ++k) {
                 const size_t j = j0 + static_cast<size_t>(k) * MSG_THREADS + threadIdx.x;
                 if (j < code_len) {
-                    uint64_t v = 0;
-                    if (j < cols) v = gl::from_i16(wr[j]);
-                    else if (j < cols + pad) v = pads[r * pad + (j - cols)];
-                    __builtin_nontemporal_store(v, o + j);
+                    uint64_t x = 0;
+                    if (j < cols) x = gl::from_i16(wr[j]);
+                    else if (j < cols + pad) x = pads[r * pad + (j - cols)];
+                    __builtin_nontemporal_store(x, o + j);
                 }
             }
         }
@@ -77,8 +104,8 @@ int pcs_messages(Context* c, const int16_t* w, const uint64_t* pads, size_t rows
     const size_t spans = (code_len + SPAN - 1) / SPAN;
     if (spans > (1u << 20)) return fail_msg(c, "message row too long for the message kernel");
     const size_t cus = c->cu_count > 0 ? static_cast<size_t>(c->cu_count) : 256;
-    // rows per span column: enough workgroups for about 64 per CU, at most one per row
-    const size_t row_groups = std::max<size_t>(1, std::min(rows, std::max<size_t>(1, cus * 64 / spans)));
+    // rows per span column: enough workgroups for about 128 per CU, at most one per row
+    const size_t row_groups = std::max<size_t>(1, std::min(rows, std::max<size_t>(1, cus * 128 / spans)));
     const unsigned blocks = static_cast<unsigned>(spans * row_groups);
     hipLaunchKernelGGL(messages_kernel, dim3(blocks), dim3(MSG_THREADS), 0, c->stream, w, pads, out, rows, cols, pad,
                        code_len, static_cast<unsigned>(spans));
