@@ -28,6 +28,7 @@ static void abort_record(Context* c) noexcept {
     if (!c) return;
     if (c->coarse_accounted) c->poisoned = true;
     if (c->record_active && c->timing_mode == TIMING_EVENTS_DEFERRED) c->ring[c->active_slot].mask = 0;
+    c->reuse_slot = -1;  // a failed primitive may have enqueued work after the last marker
     c->record_active = false;
     c->coarse_active = false;
     c->coarse_inner = false;
@@ -1119,6 +1120,7 @@ VMX_API int volta_cuda_reset_stats(void* raw) {
     }
     c->ring_begin = 0;
     c->ring_pending = 0;
+    stream_touched(c);  // no record is left to lend its marker
     const uint64_t live = c->stats.live_device_bytes;
     const uint64_t live_pinned = c->stats.live_pinned_bytes;
     c->stats = RawStats{};
