@@ -44,6 +44,12 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
     size_t row = blockIdx.x;
     if (PREFETCH && row < rows) fetch_row<NZ>(src, row, r.m, raw);
     __syncthreads();
+    // Wave priority by phase, as in the one-pass 2^13 kernel: between a row's
+    // last barrier and the next row's first one the waves run apart, and the
+    // ones storing go first (2), then the ones loading and in stage A (1),
+    // before any wave in the exchanges (0).  C4 4.85-4.93 -> 4.70-4.76 ms,
+    // p15 3.80-3.86 -> 3.72-3.78 ms, alternating on one box.
+    __builtin_amdgcn_s_setprio(1);
     for (; row < rows; row += gridDim.x) {
         // The role indices are recomputed from an opaque copy of the thread
         // index where each phase needs them (a few adds), so neither they nor
@@ -71,6 +77,7 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
             if (w0 == 0) x1_write<0>(lds, v, tw, t1, q.m);
             else x1_write<1>(lds, v, tw, t1, q.m);
         }
+        __builtin_amdgcn_s_setprio(0);  // the exchanges and stage B
         __builtin_amdgcn_sched_barrier(0);
         load_tw1<0>(tw, t1, w0 ^ 1, here().m);
         __syncthreads();
@@ -109,6 +116,7 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
             __syncthreads();
         });
         if (PREFETCH && row + gridDim.x < rows) fetch_row<NZ>(src, row + gridDim.x, here().m, raw);
+        __builtin_amdgcn_s_setprio(2);  // stage C and the stores
         __builtin_amdgcn_sched_barrier(0);
         gl::dit_pow2<5, gl::E_W32>(v);
         // X[k3 + 32 k2 + 1024 k1]: scalar offset k1 8 KiB, non-temporal (aux bit 1)
@@ -120,6 +128,7 @@ __global__ __launch_bounds__(THREADS) void ntt15_rows(Src src, size_t rows, cons
             const v2u d = {static_cast<uint32_t>(v[k1]), static_cast<uint32_t>(v[k1] >> 32)};
             __builtin_amdgcn_raw_buffer_store_b64(d, orow, qo, k1 * 8192u, 2);
         });
+        __builtin_amdgcn_s_setprio(1);  // the next row's loads, stage A and first exchange write
     }
 #endif
 }
